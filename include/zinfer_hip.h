@@ -1,0 +1,220 @@
+/*
+ * zinfer_hip.h -- C ABI of libzinfer_hip, the MI355X (gfx950) sampling and
+ * constrained-decoding path for zinfer.
+ *
+ * The reference (pylypenko99/zinfer, Zig 0.17.1) has no plugin or FFI layer;
+ * its boundary is the Zig API of src/sampler.zig, src/grammar.zig and
+ * src/gen.zig.  Each declaration below names the reference symbol it replaces
+ * (file:line).  A Zig shim binds these with `extern fn ... callconv(.c)`.
+ *
+ * Conventions
+ *  - Every entry point that can fail returns int32_t: ZI_OK (0) or a negative
+ *    zi_status.  zi_last_error() gives a static description of the last error
+ *    on the calling thread.
+ *  - "device" pointers are HIP device allocations on the context's device;
+ *    "host" pointers are ordinary process memory.
+ *  - Batched entry points (zi_*_rows) are stream-ordered on the context's
+ *    stream and return once the work is enqueued; zi_sync() waits.  Calls on
+ *    one context share its scratch memory and must not overlap (one context
+ *    per thread, as the reference keeps one Sampler per thread).
+ *  - Logit rows are row-major [rows][ld]; the logits pointer must be 16-byte
+ *    aligned and ld a multiple of 8 elements.  NaN logits are outside the
+ *    contract (the reference's insertion sort gives order-dependent results
+ *    for them); the kernels never select a NaN.
+ */
+#ifndef ZINFER_HIP_H
+#define ZINFER_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ZI_ABI_VERSION 1
+
+typedef enum zi_status {
+    ZI_OK = 0,
+    ZI_ERR_INVALID = -1,     /* bad argument (null, size, alignment) */
+    ZI_ERR_HIP = -2,         /* HIP runtime error */
+    ZI_ERR_OOM = -3,         /* device or host allocation failed */
+    ZI_ERR_UNSUPPORTED = -4, /* valid request outside what this build implements */
+    ZI_ERR_CAPACITY = -5     /* exceeds the context's max_rows / max_vocab */
+} zi_status;
+
+typedef enum zi_dtype { ZI_F32 = 0, ZI_BF16 = 1 } zi_dtype;
+
+/* Params, src/sampler.zig:3-27.  Field meaning and defaults follow the
+ * reference; usize fields are uint32_t here.  Extensions (not in the
+ * reference): freq_penalty, presence_penalty (l -= count*freq + presence for
+ * ids in the window, after the repetition penalty) and penalty_last_n (the
+ * reference fixes the window at repeat_last_n = 64, src/sampler.zig:30). */
+typedef struct zi_params {
+    float    temp;               /* 0.8  (<= 0: greedy argmax, sampler.zig:193) */
+    uint32_t top_k;              /* 40   (0: whole vocabulary) */
+    float    top_p;              /* 0.95 */
+    float    min_p;              /* 0.05 */
+    float    repeat_penalty;     /* 1.0  (1 = off) */
+    float    freq_penalty;       /* 0    extension */
+    float    presence_penalty;   /* 0    extension */
+    uint32_t penalty_last_n;     /* 64   extension (reference constant) */
+    float    dry_multiplier;     /* 0    (0 = off) */
+    float    dry_base;           /* 1.75 */
+    uint32_t dry_allowed_length; /* 2 */
+    uint32_t dry_range;          /* 1024 */
+    float    xtc_probability;    /* 0    (0 = off) */
+    float    xtc_threshold;      /* 0.1 */
+    uint32_t xtc_min_keep;       /* 1 */
+    uint64_t seed;               /* 0    (host Sampler RNG seed) */
+} zi_params;
+
+/* Fills the reference defaults (src/sampler.zig:4-26). */
+void zi_params_default(zi_params *p);
+
+/* ---------------------------------------------------------------- context */
+
+typedef struct zi_ctx zi_ctx;
+
+/* Creates a context on HIP device `device` able to serve batches of up to
+ * max_rows rows of up to max_vocab logits.  It owns a HIP stream (default
+ * priority) and the device scratch the kernels use.  No reference
+ * counterpart: the reference samples on the host (Sampler.init allocates
+ * cand[vocab], src/sampler.zig:49-58). */
+int32_t zi_create(zi_ctx **out, int32_t device, int32_t max_rows, int32_t max_vocab);
+void    zi_destroy(zi_ctx *ctx);
+/* Make batched calls use `stream` (a hipStream_t) instead of the context's
+ * own stream (the default until this is called); NULL selects HIP's default
+ * (null) stream. */
+int32_t zi_set_stream(zi_ctx *ctx, void *stream);
+int32_t zi_sync(zi_ctx *ctx);
+const char *zi_last_error(void);
+int32_t zi_abi_version(void);
+
+/* ------------------------------------------------- batched device entries */
+
+/* Per-row inputs of a batch.  All pointers are device pointers. */
+typedef struct zi_batch {
+    const void     *logits;     /* [rows][ld], f32 or bf16 */
+    int32_t         dtype;      /* zi_dtype */
+    int32_t         rows;
+    int32_t         vocab;      /* V */
+    int32_t         ld;         /* row stride in elements, >= V, multiple of 8 */
+    const uint32_t *hist;       /* [rows][hist_ld] accepted token ids, oldest first; NULL = none */
+    const int32_t  *hist_len;   /* [rows] valid entries of hist */
+    int32_t         hist_ld;
+    const uint32_t *mask;       /* [rows][mask_ld] allowed bits: id t allowed <=>
+                                   (mask[t >> 5] >> (t & 31)) & 1; NULL = all allowed */
+    int32_t         mask_ld;    /* >= ceil(V / 32) */
+    const uint32_t *edit_ids;   /* [rows][edit_ld] distinct ids whose penalized logit gets
+                                   l -= edit_delta (the DRY step); NULL = none */
+    const float    *edit_delta; /* [rows][edit_ld] */
+    const int32_t  *edit_count; /* [rows] */
+    int32_t         edit_ld;
+} zi_batch;
+
+/* Outputs of zi_sample_rows.  tok and margin are required; the rest may be
+ * NULL.  All device pointers. */
+typedef struct zi_sample_out {
+    uint32_t *tok;       /* [rows] sampled token (SampleResult.tok) */
+    float    *margin;    /* [rows] c[0].v - c[1].v, 10 if n < 2 (SampleResult.margin) */
+    int32_t  *ndraws;    /* [rows] uniforms consumed: 0 greedy, 1, 2 (XTC chance drawn) */
+    int32_t  *keep;      /* [rows] survivors after top-p and min-p */
+    uint32_t *cand_ids;  /* [rows][cand_ld] candidates in (value desc, id asc) order */
+    float    *cand_vals; /* [rows][cand_ld] their penalized logits */
+    float    *probs;     /* [rows][cand_ld] w_i / total for kept i (after XTC), else 0 */
+    int32_t   cand_ld;   /* >= top_k when the three arrays above are given */
+} zi_sample_out;
+
+/* One Sampler.sampleWithMargin (src/sampler.zig:190-276) per row, batched:
+ * mask (grammar.zig:446-479) -> repetition/frequency/presence penalty over the
+ * last penalty_last_n ids of hist (sampler.zig:91-100) -> edits (the DRY
+ * subtraction, sampler.zig:184) -> top-k -> top-p -> min-p -> temperature ->
+ * XTC -> draw.  temp <= 0 returns the reference argmax (2x8-lane tie and
+ * margin rules, sampler.zig:532-610) of the penalized row.
+ * `uniforms` [rows][2] (device) stand in for the Zig rng: the first draw is
+ * the XTC chance when XTC draws one, else the main draw; ndraws says how many
+ * were used so the caller can advance its own generator.
+ * Supported: 1 <= top_k <= 256 (or top_k = 0 / top_k > V with V <= 256),
+ * penalty window + edits <= 1024 ids. */
+int32_t zi_sample_rows(zi_ctx *ctx, const zi_params *p, const zi_batch *b,
+                       const float *uniforms, const zi_sample_out *out);
+
+/* argmaxWithMargin per row (src/sampler.zig:532-614; greedy decoding, the
+ * bench argmax at src/main.zig:690).  out_tok/out_margin follow the reference
+ * 2x8-lane rules; out_tok_low/out_margin_true (may be NULL) give the
+ * lowest-index argmax and the true top-1 minus top-2 gap.  Only logits,
+ * dtype, rows, vocab and ld of `b` are read.  Device outputs [rows]. */
+int32_t zi_argmax_rows(zi_ctx *ctx, const zi_batch *b, uint32_t *out_tok, float *out_margin,
+                       uint32_t *out_tok_low, float *out_margin_true);
+
+/* Speculative-verify row statistics (the consumer is Gen.AdaptiveDraft and
+ * the accept compare, src/gen.zig:366-432, :544-587): Shannon entropy (nats)
+ * of the T = 1 full-vocabulary softmax, the top-k ids (k <= 64, value desc,
+ * id asc) with full-vocabulary probabilities, the lowest-index argmax and,
+ * when draft (device [rows]) is non-NULL, accept[r] = (argmax == draft[r]).
+ * The reference has no entropy (it uses the logit margin); this is the new
+ * signal.  Only logits, dtype, rows, vocab, ld of `b` are read. */
+int32_t zi_entropy_topk_rows(zi_ctx *ctx, const zi_batch *b, int32_t k, const uint32_t *draft,
+                             float *out_entropy, uint32_t *out_ids, float *out_probs,
+                             int32_t out_ld, uint32_t *out_argmax, uint8_t *out_accept);
+
+/* JsonValidator.applyMask (src/grammar.zig:446-479) for a precomputed packed
+ * mask: logits[r][t] = -inf where the bit is clear, in place (f32 or bf16).
+ * Only logits, dtype, rows, vocab, ld, mask, mask_ld of `b` are read. */
+int32_t zi_apply_mask_rows(zi_ctx *ctx, const zi_batch *b);
+
+/* ------------------------------------------ host mirror of the Zig Sampler */
+
+/* The Sampler of src/sampler.zig:38-286 with the same state (params, RNG,
+ * 64-entry recent ring, 4096-entry history, breakers) and methods; each
+ * sample call runs zi_sample_rows on one host row.  The RNG restates Zig's
+ * DefaultPrng (xoshiro256++ seeded by splitmix64) and Random.float(f32). */
+typedef struct zi_sampler zi_sampler;
+
+int32_t zi_sampler_init(zi_sampler **out, zi_ctx *ctx, uint32_t vocab, const zi_params *p); /* :49 */
+void    zi_sampler_deinit(zi_sampler *s);                                                  /* :60 */
+void    zi_sampler_reset(zi_sampler *s);                                                   /* :64 */
+void    zi_sampler_add_breaker(zi_sampler *s, uint32_t tok);                               /* :69 */
+int32_t zi_sampler_is_breaker(const zi_sampler *s, uint32_t tok);                          /* :76 */
+void    zi_sampler_accept(zi_sampler *s, uint32_t tok);                                    /* :84 */
+/* Host DRY step on host logits, in place (src/sampler.zig:104-187). */
+void    zi_sampler_apply_dry(const zi_sampler *s, float *logits, uint32_t n);
+/* sampleWithMargin (src/sampler.zig:190): host logits, modified in place by
+ * the penalty and DRY exactly as the reference modifies them. */
+int32_t zi_sampler_sample_with_margin(zi_sampler *s, float *logits, uint32_t n, uint32_t *tok,
+                                      float *margin);
+int32_t zi_sampler_sample(zi_sampler *s, float *logits, uint32_t n, uint32_t *tok); /* :279 */
+/* Read / replace the params (server.zig:377-415 writes g.smp.p fields). */
+void    zi_sampler_get_params(const zi_sampler *s, zi_params *p);
+void    zi_sampler_set_params(zi_sampler *s, const zi_params *p);
+/* rng = DefaultPrng.init(seed) (sampler.zig:52, server.zig:414). */
+void    zi_sampler_seed(zi_sampler *s, uint64_t seed);
+/* Next Random.float(f32) of the sampler's generator (advances it). */
+float   zi_sampler_rand_f32(zi_sampler *s);
+
+/* argmaxWithMargin on a host row (src/sampler.zig:532-614); synchronous. */
+int32_t zi_argmax_with_margin(zi_ctx *ctx, const float *logits, uint32_t n, uint32_t *tok,
+                              float *margin);
+
+/* DRY edits (src/sampler.zig:104-187) from a linear history (oldest first),
+ * as (id, delta) pairs for zi_batch.edit_*; returns the count (<= 128). */
+uint32_t zi_dry_edits(const uint32_t *hist, uint32_t n_hist, const uint32_t *breakers,
+                      uint32_t n_breakers, const zi_params *p, uint32_t *out_ids,
+                      float *out_deltas);
+
+/* Gen.AdaptiveDraft (src/gen.zig:366-432), host-side. */
+typedef struct zi_adaptive_draft {
+    uint64_t cur_k, max_k, min_k, consecutive_rejections, cooldown_steps;
+    float    last_margin;
+} zi_adaptive_draft;
+void     zi_adaptive_draft_init(zi_adaptive_draft *a, uint64_t max_k);           /* :374 */
+void     zi_adaptive_draft_record_margin(zi_adaptive_draft *a, float margin);    /* :382 */
+uint64_t zi_adaptive_draft_next(zi_adaptive_draft *a);                           /* :388 */
+void     zi_adaptive_draft_update(zi_adaptive_draft *a, uint64_t accepted, uint64_t drafted,
+                                  int32_t has_margin, float margin);             /* :408 */
+
+#ifdef __cplusplus
+}
+#endif
+#endif

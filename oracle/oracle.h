@@ -1,0 +1,166 @@
+/*
+ * oracle.h -- CPU restatement of zinfer's sampling / constrained-decoding path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product (zinfer_amd/, include/)
+ * links, loads or calls this code.  Only tests/, __graft_entry__.smoke() and
+ * bench.py's cpu_baseline leg use it, as the checker and as the timed CPU
+ * baseline ("port").
+ *
+ * The reference (pylypenko99/zinfer) is Zig 0.17.1; no Zig toolchain exists in
+ * this image, so the reference cannot be built (oracle/_ref stays empty).  Each
+ * function below restates one reference function, cited file:line relative to
+ * the reference repository root, in plain C with the same sequential f32
+ * arithmetic.  Compile with -ffp-contract=off (no FMA contraction): every
+ * product and sum must round on its own, as in the Zig source.
+ *
+ * Pinning status (how each function is checked before it is trusted):
+ *   or_argmax_with_margin  pinned: reference KAT sampler.zig:616-632, plus an
+ *                          independent numpy model of the 2x8-lane reduction on
+ *                          tie-heavy inputs.
+ *   or_apply_penalty       pinned: closed forms (l/rp, l*rp, count*freq+pres) on
+ *                          crafted windows.
+ *   or_dry_edits           pinned: reference KAT sampler.zig:634-673 (9.2, 8.4,
+ *                          breaker keeps 10.0) and brute-force longest-suffix match.
+ *   or_sample              pinned: KATs sampler.zig:675-702 (min-p) and :704-748
+ *                          (XTC); top-k order vs numpy lexsort; top-p keep vs numpy
+ *                          float32 add.accumulate; draw vs inverse-CDF on
+ *                          float32 running remainders; empirical draw frequencies.
+ *   or_apply_mask          pinned: closed form (bit test -> -inf).
+ *   or_entropy_topk        pinned: scipy.stats.entropy(softmax) and brute-force top-k.
+ *   or_adaptive_*          pinned: reference KAT gen.zig:845-874.
+ *   or_rng_*               PARITY UNPINNED for the Zig DefaultPrng stream (no Zig
+ *                          here, no reference vectors); splitmix64 alone is pinned
+ *                          by its published sequence for seed 1234567.
+ *   exp                    Zig @exp (compiler-rt expf) last-ulp bits are PARITY
+ *                          UNPINNED; both this oracle and the device tail use
+ *                          or_exp32 = (float)exp((double)x), correctly rounded in
+ *                          practice.
+ */
+#ifndef ZINFER_ORACLE_H
+#define ZINFER_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Params, src/sampler.zig:3-27, plus the frequency/presence extension and the
+ * penalty window (fixed at 64 in the reference, src/sampler.zig:30). */
+typedef struct or_params {
+    float    temp;
+    uint32_t top_k;
+    float    top_p;
+    float    min_p;
+    float    repeat_penalty;
+    float    freq_penalty;
+    float    presence_penalty;
+    uint32_t penalty_last_n;
+    float    dry_multiplier;
+    float    dry_base;
+    uint32_t dry_allowed_length;
+    uint32_t dry_range;
+    float    xtc_probability;
+    float    xtc_threshold;
+    uint32_t xtc_min_keep;
+} or_params;
+
+/* SampleResult, src/sampler.zig:527-530 */
+typedef struct or_result {
+    uint32_t tok;
+    float    margin;
+} or_result;
+
+typedef struct or_sample_diag {
+    int32_t   ndraws; /* uniforms consumed: 0 (greedy), 1, or 2 (XTC chance drawn) */
+    int32_t   n;      /* candidates after top-k */
+    int32_t   keep;   /* after top-p and min-p */
+    int32_t   start;  /* XTC start index */
+    float     total;  /* weight total the draw scales */
+    int32_t   cap;    /* capacity of ids/vals/probs (0 = none) */
+    uint32_t *ids;    /* candidate ids in order */
+    float    *vals;   /* penalized logits in order */
+    float    *probs;  /* w_i / total for start <= i < keep, else 0 */
+} or_sample_diag;
+
+float or_exp32(float x);
+
+void or_params_default(or_params *p);
+
+/* src/sampler.zig:91-100 (+ frequency/presence extension, window = caller's). */
+void or_apply_penalty(float *logits, uint32_t V, const uint32_t *window, uint32_t n,
+                      float rp, float freq, float pres);
+
+/* Subtractive sparse edits: logits[id] -= delta (the DRY step, src/sampler.zig:184). */
+void or_apply_edits(float *logits, uint32_t V, const uint32_t *ids, const float *deltas,
+                    uint32_t n);
+
+/* src/sampler.zig:104-187: DRY edits from a linear history (oldest first). */
+uint32_t or_dry_edits(const uint32_t *hist, uint32_t n_hist, const uint32_t *breakers,
+                      uint32_t n_breakers, float mult, float base, uint32_t allowed,
+                      uint32_t range, uint32_t *out_ids, float *out_deltas);
+
+/* src/grammar.zig:446-479 restated for a packed allowed-mask:
+ * id allowed <=> (words[id >> 5] >> (id & 31)) & 1. */
+void or_apply_mask(float *logits, uint32_t V, const uint32_t *words);
+
+/* src/sampler.zig:532-610 (2x8-lane SIMD tie and margin semantics). */
+or_result or_argmax_with_margin(const float *x, uint32_t n);
+
+/* Lowest-index argmax with the true top-1 minus top-2 gap (new semantics). */
+or_result or_argmax_true(const float *x, uint32_t n);
+
+/* src/sampler.zig:190-276 after the penalty, with injected uniforms u[0], u[1]
+ * standing in for the first and second rng.float(f32) draws.  `logits` is the
+ * already-penalized row; it is not modified. */
+or_result or_sample_penalized(const or_params *p, const float *logits, uint32_t V,
+                              const float *u, or_sample_diag *diag);
+
+/* Whole-row pipeline as gen.zig drives it: mask (optional), penalty over the
+ * window, sparse edits, then or_sample_penalized.  `logits` is modified in place
+ * like the reference's sampleWithMargin. */
+or_result or_sample_row(const or_params *p, float *logits, uint32_t V, const uint32_t *mask,
+                        const uint32_t *window, uint32_t n_window, const uint32_t *edit_ids,
+                        const float *edit_deltas, uint32_t n_edits, const float *u,
+                        or_sample_diag *diag);
+
+/* New semantics (entropy of the T=1 full-vocab softmax, nats; top-k ids in
+ * (value desc, id asc) order with full-vocab normalized probabilities). */
+void or_entropy_topk(const float *x, uint32_t V, uint32_t k, double *entropy, uint32_t *ids,
+                     double *probs);
+
+/* gen.zig:366-432 AdaptiveDraft */
+typedef struct or_adaptive {
+    uint64_t cur_k, max_k, min_k, consecutive_rejections, cooldown_steps;
+    float    last_margin;
+} or_adaptive;
+void     or_adaptive_init(or_adaptive *a, uint64_t max_k);
+void     or_adaptive_record_margin(or_adaptive *a, float m);
+uint64_t or_adaptive_next(or_adaptive *a);
+void     or_adaptive_update(or_adaptive *a, uint64_t accepted, uint64_t drafted, int has_margin,
+                            float margin);
+
+/* Zig std.Random.DefaultPrng restated from the published algorithms
+ * (xoshiro256++ seeded by splitmix64) and Random.float(f32). */
+uint64_t or_splitmix64_next(uint64_t *state);
+void     or_xoshiro_seed(uint64_t s[4], uint64_t seed);
+uint64_t or_xoshiro_next(uint64_t s[4]);
+float    or_rand_f32(uint64_t s[4]);
+
+/* CPU baseline: sample `rows` rows (row stride ld), histories [rows][hist_ld]
+ * with hist_len[row] valid entries (window = last penalty_last_n), optional
+ * masks [rows][mask_ld], uniforms [rows][2].  Rows are copied into a scratch
+ * row before the in-place pipeline so the inputs stay unchanged; the copy is
+ * excluded from the returned seconds.  Returns elapsed seconds over `reps`
+ * passes. */
+double or_bench_sample_rows(const or_params *p, const float *logits, uint32_t rows, uint32_t V,
+                            uint64_t ld, const uint32_t *hist, const int32_t *hist_len,
+                            uint32_t hist_ld, const uint32_t *mask, uint32_t mask_ld,
+                            const float *uniforms, uint32_t reps, uint32_t *out_tok,
+                            float *out_margin);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,209 @@
+"""Torch-facing wrappers over the C ABI (device memory and streams only).
+
+Tensors are passed to libzinfer_hip as raw device pointers; every call is
+enqueued on torch's current stream so it orders with the surrounding torch
+work.  Nothing here computes a result on the host.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._lib import ZiBatch, ZiParams, ZiSampleOut, check, lib
+
+__all__ = ["Context", "Sampler", "params", "SampleResult"]
+
+params = _lib.params
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    if t.dtype == torch.float32:
+        return _lib.ZI_F32
+    if t.dtype == torch.bfloat16:
+        return _lib.ZI_BF16
+    raise TypeError(f"logits dtype {t.dtype} (need float32 or bfloat16)")
+
+
+@dataclass
+class SampleResult:
+    tok: torch.Tensor
+    margin: torch.Tensor
+    ndraws: torch.Tensor
+    keep: Optional[torch.Tensor] = None
+    cand_ids: Optional[torch.Tensor] = None
+    cand_vals: Optional[torch.Tensor] = None
+    probs: Optional[torch.Tensor] = None
+
+
+class Context:
+    """zi_ctx: device scratch + stream for batches of <= max_rows x max_vocab."""
+
+    def __init__(self, device: int = 0, max_rows: int = 512, max_vocab: int = 262144):
+        self.device = device
+        h = C.c_void_p()
+        check(lib().zi_create(C.byref(h), device, max_rows, max_vocab))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().zi_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _bind_stream(self):
+        s = torch.cuda.current_stream(self.device)
+        check(lib().zi_set_stream(self.h, C.c_void_p(s.cuda_stream)))
+
+    @staticmethod
+    def batch(logits: torch.Tensor, vocab: Optional[int] = None, hist=None, hist_len=None, mask=None,
+              edit_ids=None, edit_delta=None, edit_count=None) -> ZiBatch:
+        assert logits.dim() == 2 and logits.stride(1) == 1
+        b = ZiBatch()
+        b.logits = logits.data_ptr()
+        b.dtype = _dtype_code(logits)
+        b.rows = logits.shape[0]
+        b.vocab = logits.shape[1] if vocab is None else vocab
+        b.ld = logits.stride(0)
+        if hist is not None:
+            b.hist, b.hist_len, b.hist_ld = hist.data_ptr(), hist_len.data_ptr(), hist.stride(0)
+        if mask is not None:
+            b.mask, b.mask_ld = mask.data_ptr(), mask.stride(0)
+        if edit_ids is not None:
+            b.edit_ids, b.edit_delta, b.edit_count = edit_ids.data_ptr(), edit_delta.data_ptr(), edit_count.data_ptr()
+            b.edit_ld = edit_ids.stride(0)
+        return b
+
+    def sample_rows(self, p: ZiParams, logits: torch.Tensor, uniforms: torch.Tensor, *, vocab=None, hist=None,
+                    hist_len=None, mask=None, edit_ids=None, edit_delta=None, edit_count=None,
+                    cands: bool = False, out: Optional[SampleResult] = None) -> SampleResult:
+        rows = logits.shape[0]
+        dev = logits.device
+        if out is None:
+            out = SampleResult(tok=torch.empty(rows, dtype=torch.int32, device=dev),
+                               margin=torch.empty(rows, dtype=torch.float32, device=dev),
+                               ndraws=torch.empty(rows, dtype=torch.int32, device=dev))
+            if cands:
+                V = logits.shape[1] if vocab is None else vocab
+                k = V if (p.top_k == 0 or p.top_k > V) else p.top_k
+                out.keep = torch.empty(rows, dtype=torch.int32, device=dev)
+                out.cand_ids = torch.full((rows, k), -1, dtype=torch.int32, device=dev)
+                out.cand_vals = torch.zeros((rows, k), dtype=torch.float32, device=dev)
+                out.probs = torch.zeros((rows, k), dtype=torch.float32, device=dev)
+        o = ZiSampleOut()
+        o.tok, o.margin, o.ndraws = out.tok.data_ptr(), out.margin.data_ptr(), out.ndraws.data_ptr()
+        if out.keep is not None:
+            o.keep = out.keep.data_ptr()
+        if out.cand_ids is not None:
+            o.cand_ids, o.cand_vals, o.probs = out.cand_ids.data_ptr(), out.cand_vals.data_ptr(), out.probs.data_ptr()
+            o.cand_ld = out.cand_ids.stride(0)
+        b = self.batch(logits, vocab, hist, hist_len, mask, edit_ids, edit_delta, edit_count)
+        self._bind_stream()
+        check(lib().zi_sample_rows(self.h, C.byref(p), C.byref(b), _ptr(uniforms), C.byref(o)))
+        return out
+
+    def argmax_rows(self, logits: torch.Tensor, vocab=None):
+        rows, dev = logits.shape[0], logits.device
+        tok = torch.empty(rows, dtype=torch.int32, device=dev)
+        margin = torch.empty(rows, dtype=torch.float32, device=dev)
+        tok_low = torch.empty(rows, dtype=torch.int32, device=dev)
+        margin_true = torch.empty(rows, dtype=torch.float32, device=dev)
+        b = self.batch(logits, vocab)
+        self._bind_stream()
+        check(lib().zi_argmax_rows(self.h, C.byref(b), _ptr(tok), _ptr(margin), _ptr(tok_low), _ptr(margin_true)))
+        return tok, margin, tok_low, margin_true
+
+    def entropy_topk_rows(self, logits: torch.Tensor, k: int, draft: Optional[torch.Tensor] = None, vocab=None):
+        rows, dev = logits.shape[0], logits.device
+        ent = torch.empty(rows, dtype=torch.float32, device=dev)
+        ids = torch.empty((rows, k), dtype=torch.int32, device=dev)
+        probs = torch.empty((rows, k), dtype=torch.float32, device=dev)
+        am = torch.empty(rows, dtype=torch.int32, device=dev)
+        acc = torch.empty(rows, dtype=torch.uint8, device=dev) if draft is not None else None
+        b = self.batch(logits, vocab)
+        self._bind_stream()
+        check(lib().zi_entropy_topk_rows(self.h, C.byref(b), k, _ptr(draft), _ptr(ent), _ptr(ids), _ptr(probs), k,
+                                         _ptr(am), _ptr(acc)))
+        return ent, ids, probs, am, acc
+
+    def apply_mask_rows(self, logits: torch.Tensor, mask: torch.Tensor, vocab=None):
+        b = self.batch(logits, vocab, mask=mask)
+        self._bind_stream()
+        check(lib().zi_apply_mask_rows(self.h, C.byref(b)))
+        return logits
+
+
+class Sampler:
+    """The host mirror of the Zig Sampler (zi_sampler_*), one host row per call."""
+
+    def __init__(self, ctx: Context, vocab: int, p: ZiParams):
+        self.ctx = ctx
+        self.vocab = vocab
+        h = C.c_void_p()
+        check(lib().zi_sampler_init(C.byref(h), ctx.h, vocab, C.byref(p)))
+        self.h = h
+
+    def __del__(self):
+        try:
+            if self.h:
+                lib().zi_sampler_deinit(self.h)
+                self.h = None
+        except Exception:
+            pass
+
+    def reset(self):
+        lib().zi_sampler_reset(self.h)
+
+    def add_breaker(self, tok: int):
+        lib().zi_sampler_add_breaker(self.h, tok)
+
+    def is_breaker(self, tok: int) -> bool:
+        return bool(lib().zi_sampler_is_breaker(self.h, tok))
+
+    def accept(self, tok: int):
+        lib().zi_sampler_accept(self.h, tok)
+
+    def seed(self, s: int):
+        lib().zi_sampler_seed(self.h, s)
+
+    def rand_f32(self) -> float:
+        return float(lib().zi_sampler_rand_f32(self.h))
+
+    def apply_dry(self, logits):
+        import numpy as np
+        a = np.ascontiguousarray(logits, dtype=np.float32)
+        lib().zi_sampler_apply_dry(self.h, a.ctypes.data_as(_lib.f32p), a.size)
+        return a
+
+    def sample_with_margin(self, logits):
+        """logits: a float32 numpy array; modified in place like the reference."""
+        import numpy as np
+        assert isinstance(logits, np.ndarray) and logits.dtype == np.float32 and logits.flags.c_contiguous
+        tok = C.c_uint32()
+        m = C.c_float()
+        check(lib().zi_sampler_sample_with_margin(self.h, logits.ctypes.data_as(_lib.f32p), logits.size,
+                                                  C.byref(tok), C.byref(m)))
+        return int(tok.value), float(m.value)
+
+    def sample(self, logits) -> int:
+        return self.sample_with_margin(logits)[0]
+
+    def get_params(self) -> ZiParams:
+        p = ZiParams()
+        lib().zi_sampler_get_params(self.h, C.byref(p))
+        return p
+
+    def set_params(self, p: ZiParams):
+        lib().zi_sampler_set_params(self.h, C.byref(p))

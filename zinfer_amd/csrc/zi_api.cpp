@@ -1,0 +1,359 @@
+// zi_api.cpp -- C ABI of libzinfer_hip: context, argument checks, chunk
+// planning and kernel dispatch for the batched device entry points.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "../../include/zinfer_hip.h"
+#include "zi_internal.hpp"
+#include "zi_launch.hpp"
+
+namespace {
+thread_local char g_err[512] = "no error";
+}
+
+int32_t zi_fail(int32_t code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int32_t zi_hip_fail(hipError_t e, const char *what) {
+    return zi_fail(ZI_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+extern "C" const char *zi_last_error(void) { return g_err; }
+extern "C" int32_t zi_abi_version(void) { return ZI_ABI_VERSION; }
+
+extern "C" void zi_params_default(zi_params *p) {
+    if (!p) return;
+    std::memset(p, 0, sizeof *p);
+    p->temp = 0.8f;  // src/sampler.zig:4-26
+    p->top_k = 40;
+    p->top_p = 0.95f;
+    p->min_p = 0.05f;
+    p->repeat_penalty = 1.0f;
+    p->freq_penalty = 0.0f;
+    p->presence_penalty = 0.0f;
+    p->penalty_last_n = 64;  // repeat_last_n, src/sampler.zig:30
+    p->dry_multiplier = 0.0f;
+    p->dry_base = 1.75f;
+    p->dry_allowed_length = 2;
+    p->dry_range = 1024;
+    p->xtc_probability = 0.0f;
+    p->xtc_threshold = 0.1f;
+    p->xtc_min_keep = 1;
+    p->seed = 0;
+}
+
+#define HIP_TRY(call, what)                          \
+    do {                                             \
+        hipError_t e_ = (call);                      \
+        if (e_ != hipSuccess) return zi_hip_fail(e_, what); \
+    } while (0)
+
+extern "C" int32_t zi_create(zi_ctx **out, int32_t device, int32_t max_rows, int32_t max_vocab) {
+    if (!out) return zi_fail(ZI_ERR_INVALID, "zi_create: out is NULL");
+    *out = nullptr;
+    if (max_rows < 1 || max_vocab < 1)
+        return zi_fail(ZI_ERR_INVALID, "zi_create: max_rows=%d max_vocab=%d", max_rows, max_vocab);
+    if (max_vocab > zi::kMaxVocab)
+        return zi_fail(ZI_ERR_UNSUPPORTED, "zi_create: max_vocab %d > %d", max_vocab, zi::kMaxVocab);
+    int ndev = 0;
+    HIP_TRY(hipGetDeviceCount(&ndev), "hipGetDeviceCount");
+    if (device < 0 || device >= ndev)
+        return zi_fail(ZI_ERR_INVALID, "zi_create: device %d of %d", device, ndev);
+    HIP_TRY(hipSetDevice(device), "hipSetDevice");
+
+    zi_ctx *c = new (std::nothrow) zi_ctx();
+    if (!c) return zi_fail(ZI_ERR_OOM, "zi_create: host allocation");
+    c->device = device;
+    c->max_rows = max_rows;
+    c->max_vocab = max_vocab;
+    hipError_t e = hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete c;
+        return zi_hip_fail(e, "hipStreamCreate");
+    }
+    c->stream = c->own_stream;
+
+    const size_t R = (size_t)max_rows, G = zi::kMaxGHost, CAP = zi::kCapAHost;
+    struct Buf {
+        void **p;
+        size_t bytes;
+    } bufs[] = {
+        {(void **)&c->g_key, R * G * CAP * sizeof(uint64_t)},
+        {(void **)&c->g_val, R * G * CAP * sizeof(float)},
+        {(void **)&c->g_cnt, R * G * sizeof(int32_t)},
+        {(void **)&c->tickets, R * sizeof(int32_t)},
+        {(void **)&c->g_stat, R * G * 3 * sizeof(double)},
+        {(void **)&c->g_cls, R * G * 16 * sizeof(uint64_t)},
+        {(void **)&c->g_raw, R * G * 16 * sizeof(uint32_t)},
+        {(void **)&c->g_top2, R * G * 2 * sizeof(float)},
+        {(void **)&c->g_tail, R * 16 * sizeof(float)},
+    };
+    for (auto &b : bufs) {
+        e = hipMalloc(b.p, b.bytes);
+        if (e != hipSuccess) {
+            zi_destroy(c);
+            return zi_fail(ZI_ERR_OOM, "zi_create: hipMalloc %zu bytes: %s", b.bytes, hipGetErrorString(e));
+        }
+    }
+    e = hipMemset(c->tickets, 0, R * sizeof(int32_t));
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        zi_destroy(c);
+        return zi_hip_fail(e, "zi_create: clear tickets");
+    }
+    *out = c;
+    return ZI_OK;
+}
+
+extern "C" void zi_destroy(zi_ctx *c) {
+    if (!c) return;
+    hipSetDevice(c->device);
+    if (c->own_stream) hipStreamSynchronize(c->own_stream);
+    void *ptrs[] = {c->g_key, c->g_val, c->g_cnt, c->tickets, c->g_stat, c->g_cls, c->g_raw, c->g_top2, c->g_tail};
+    for (void *p : ptrs)
+        if (p) hipFree(p);
+    if (c->own_stream) hipStreamDestroy(c->own_stream);
+    delete c;
+}
+
+extern "C" int32_t zi_set_stream(zi_ctx *c, void *stream) {
+    if (!c) return zi_fail(ZI_ERR_INVALID, "zi_set_stream: ctx is NULL");
+    c->stream = (hipStream_t)stream;  // NULL is HIP's default (null) stream
+    return ZI_OK;
+}
+
+extern "C" int32_t zi_sync(zi_ctx *c) {
+    if (!c) return zi_fail(ZI_ERR_INVALID, "zi_sync: ctx is NULL");
+    HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+    HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return ZI_OK;
+}
+
+namespace zi {
+
+// Chunking: 256 threads x EPT elements per workgroup, EPT in {16, 32, 64};
+// the largest EPT that still gives >= 512 workgroups (or EPT 16), with at
+// most kMaxG chunks per row.
+Plan plan_rows(int rows, int V, int dtype) {
+    Plan pl;
+    const int vec = dtype == ZI_F32 ? 4 : 8;
+    int ept = 64;
+    auto chunks = [&](int e) { return (V + kThreadsHost * e - 1) / (kThreadsHost * e); };
+    while (ept > 16 && (int64_t)rows * chunks(ept) < 512 && chunks(ept / 2) <= kMaxGHost) ept /= 2;
+    int G = chunks(ept);
+    int CH = (V + G - 1) / G;
+    CH = (CH + 63) / 64 * 64;
+    G = (V + CH - 1) / CH;
+    pl.G = G;
+    pl.CH = CH;
+    pl.nv = ept / vec;
+    return pl;
+}
+
+}  // namespace zi
+
+static int32_t check_batch(const zi_ctx *c, const zi_batch *b, const char *fn) {
+    if (!c || !b) return zi_fail(ZI_ERR_INVALID, "%s: NULL ctx or batch", fn);
+    if (!b->logits) return zi_fail(ZI_ERR_INVALID, "%s: logits is NULL", fn);
+    if (b->dtype != ZI_F32 && b->dtype != ZI_BF16) return zi_fail(ZI_ERR_INVALID, "%s: dtype %d", fn, b->dtype);
+    if (b->rows < 1 || b->vocab < 1) return zi_fail(ZI_ERR_INVALID, "%s: rows=%d vocab=%d", fn, b->rows, b->vocab);
+    if (b->rows > c->max_rows || b->vocab > c->max_vocab)
+        return zi_fail(ZI_ERR_CAPACITY, "%s: rows=%d vocab=%d exceed context (%d, %d)", fn, b->rows, b->vocab,
+                       c->max_rows, c->max_vocab);
+    if (b->ld < b->vocab || (b->ld % 8) != 0)
+        return zi_fail(ZI_ERR_INVALID, "%s: ld=%d must be >= vocab and a multiple of 8", fn, b->ld);
+    if (((uintptr_t)b->logits & 15u) != 0) return zi_fail(ZI_ERR_INVALID, "%s: logits not 16-byte aligned", fn);
+    return ZI_OK;
+}
+
+static int32_t fill_source(const zi_batch *b, const zi_params *p, bool with_inputs, zi::RowSource &s,
+                           const zi::Plan &pl, const char *fn) {
+    std::memset(&s, 0, sizeof s);
+    s.logits = b->logits;
+    s.ld = b->ld;
+    s.V = b->vocab;
+    s.G = pl.G;
+    s.CH = pl.CH;
+    s.rp = 1.0f;
+    if (!with_inputs) return ZI_OK;
+    if (b->mask) {
+        if (b->mask_ld < (b->vocab + 31) / 32)
+            return zi_fail(ZI_ERR_INVALID, "%s: mask_ld=%d < ceil(V/32)", fn, b->mask_ld);
+        s.mask = b->mask;
+        s.mask_ld = b->mask_ld;
+    }
+    if (p) {
+        s.rp = p->repeat_penalty;
+        s.freq = p->freq_penalty;
+        s.pres = p->presence_penalty;
+        s.do_rep = p->repeat_penalty != 1.0f;
+        s.do_fp = (p->freq_penalty != 0.0f || p->presence_penalty != 0.0f);
+        if (b->hist && (s.do_rep || s.do_fp) && p->penalty_last_n > 0) {
+            if (!b->hist_len || b->hist_ld < 0)
+                return zi_fail(ZI_ERR_INVALID, "%s: hist without hist_len/hist_ld", fn);
+            if (p->penalty_last_n > (uint32_t)zi::kMaxWinHost)
+                return zi_fail(ZI_ERR_UNSUPPORTED, "%s: penalty_last_n %u > %d", fn, p->penalty_last_n,
+                               zi::kMaxWinHost);
+            s.hist = b->hist;
+            s.hist_len = b->hist_len;
+            s.hist_ld = b->hist_ld;
+            s.win = (int)p->penalty_last_n;
+        }
+    }
+    if (b->edit_ids) {
+        if (!b->edit_delta || !b->edit_count || b->edit_ld < 0)
+            return zi_fail(ZI_ERR_INVALID, "%s: edit_ids without edit_delta/edit_count", fn);
+        s.edit_ids = b->edit_ids;
+        s.edit_delta = b->edit_delta;
+        s.edit_count = b->edit_count;
+        s.edit_ld = b->edit_ld;
+    }
+    return ZI_OK;
+}
+
+static int32_t run_argmax(zi_ctx *c, const zi::RowSource &src, const zi_batch *b, const zi::Plan &pl,
+                          uint32_t *tok, float *margin, uint32_t *tok_low, float *margin_true, int32_t *ndraws) {
+    zi::ArgmaxParams P;
+    std::memset(&P, 0, sizeof P);
+    P.src = src;
+    P.tok = tok;
+    P.margin = margin;
+    P.tok_low = tok_low;
+    P.margin_true = margin_true;
+    P.ndraws = ndraws;
+    P.g_cls = c->g_cls;
+    P.g_raw = c->g_raw;
+    P.g_top2 = c->g_top2;
+    P.g_tail = c->g_tail;
+    P.tickets = c->tickets;
+    hipError_t e = zi::launch_argmax(P, b->dtype, pl.nv, b->rows, c->stream);
+    if (e != hipSuccess) return zi_hip_fail(e, "argmax kernel launch");
+    return ZI_OK;
+}
+
+extern "C" int32_t zi_sample_rows(zi_ctx *c, const zi_params *p, const zi_batch *b, const float *uniforms,
+                                  const zi_sample_out *out) {
+    int32_t rc = check_batch(c, b, "zi_sample_rows");
+    if (rc) return rc;
+    if (!p || !out || !out->tok || !out->margin)
+        return zi_fail(ZI_ERR_INVALID, "zi_sample_rows: NULL params/out/tok/margin");
+    HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+    const zi::Plan pl = zi::plan_rows(b->rows, b->vocab, b->dtype);
+    zi::RowSource src;
+    rc = fill_source(b, p, true, src, pl, "zi_sample_rows");
+    if (rc) return rc;
+
+    if (p->temp <= 0.0f)  // greedy: argmax of the penalized row (src/sampler.zig:193)
+        return run_argmax(c, src, b, pl, out->tok, out->margin, nullptr, nullptr, out->ndraws);
+
+    if (!uniforms) return zi_fail(ZI_ERR_INVALID, "zi_sample_rows: uniforms is NULL");
+    const uint32_t V = (uint32_t)b->vocab;
+    const uint32_t k = (p->top_k == 0 || p->top_k > V) ? V : p->top_k;  // src/sampler.zig:197
+    if (k > (uint32_t)zi::kMaxTopK)
+        return zi_fail(ZI_ERR_UNSUPPORTED, "zi_sample_rows: top-k size %u > %d is not implemented", k,
+                       zi::kMaxTopK);
+    if ((out->cand_ids || out->cand_vals || out->probs) && out->cand_ld < (int32_t)k)
+        return zi_fail(ZI_ERR_INVALID, "zi_sample_rows: cand_ld=%d < k=%u", out->cand_ld, k);
+
+    zi::SampleParams P;
+    std::memset(&P, 0, sizeof P);
+    P.src = src;
+    P.k = (int)k;
+    P.temp = p->temp;
+    P.top_p = p->top_p;
+    P.min_p = p->min_p;
+    P.xtc_p = p->xtc_probability;
+    P.xtc_thr = p->xtc_threshold;
+    P.xtc_min_keep = (int)(p->xtc_min_keep > 0x7FFFFFFFu ? 0x7FFFFFFFu : p->xtc_min_keep);
+    P.uniforms = uniforms;
+    P.tok = out->tok;
+    P.margin = out->margin;
+    P.ndraws = out->ndraws;
+    P.keep = out->keep;
+    P.cand_ids = out->cand_ids;
+    P.cand_vals = out->cand_vals;
+    P.probs = out->probs;
+    P.cand_ld = out->cand_ld;
+    P.g_key = c->g_key;
+    P.g_val = c->g_val;
+    P.g_cnt = c->g_cnt;
+    P.tickets = c->tickets;
+    hipError_t e = zi::launch_sample(P, b->dtype, pl.nv, b->rows, c->stream);
+    if (e != hipSuccess) return zi_hip_fail(e, "sample kernel launch");
+    return ZI_OK;
+}
+
+extern "C" int32_t zi_argmax_rows(zi_ctx *c, const zi_batch *b, uint32_t *out_tok, float *out_margin,
+                                  uint32_t *out_tok_low, float *out_margin_true) {
+    int32_t rc = check_batch(c, b, "zi_argmax_rows");
+    if (rc) return rc;
+    if (!out_tok && !out_margin && !out_tok_low && !out_margin_true)
+        return zi_fail(ZI_ERR_INVALID, "zi_argmax_rows: no output");
+    HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+    const zi::Plan pl = zi::plan_rows(b->rows, b->vocab, b->dtype);
+    zi::RowSource src;
+    rc = fill_source(b, nullptr, false, src, pl, "zi_argmax_rows");
+    if (rc) return rc;
+    return run_argmax(c, src, b, pl, out_tok, out_margin, out_tok_low, out_margin_true, nullptr);
+}
+
+extern "C" int32_t zi_entropy_topk_rows(zi_ctx *c, const zi_batch *b, int32_t k, const uint32_t *draft,
+                                        float *out_entropy, uint32_t *out_ids, float *out_probs, int32_t out_ld,
+                                        uint32_t *out_argmax, uint8_t *out_accept) {
+    int32_t rc = check_batch(c, b, "zi_entropy_topk_rows");
+    if (rc) return rc;
+    if (k < 1 || k > zi::kMaxEntropyK)
+        return zi_fail(ZI_ERR_INVALID, "zi_entropy_topk_rows: k=%d outside [1, %d]", k, zi::kMaxEntropyK);
+    if ((out_ids || out_probs) && out_ld < k)
+        return zi_fail(ZI_ERR_INVALID, "zi_entropy_topk_rows: out_ld=%d < k=%d", out_ld, k);
+    if (out_accept && !draft) return zi_fail(ZI_ERR_INVALID, "zi_entropy_topk_rows: out_accept needs draft");
+    HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+    const zi::Plan pl = zi::plan_rows(b->rows, b->vocab, b->dtype);
+    zi::EntropyParams P;
+    std::memset(&P, 0, sizeof P);
+    rc = fill_source(b, nullptr, false, P.src, pl, "zi_entropy_topk_rows");
+    if (rc) return rc;
+    P.k = k;
+    P.draft = draft;
+    P.entropy = out_entropy;
+    P.ids = out_ids;
+    P.probs = out_probs;
+    P.out_ld = out_ld;
+    P.argmax = out_argmax;
+    P.accept = out_accept;
+    P.g_key = c->g_key;
+    P.g_val = c->g_val;
+    P.g_cnt = c->g_cnt;
+    P.g_stat = c->g_stat;
+    P.tickets = c->tickets;
+    hipError_t e = zi::launch_entropy(P, b->dtype, pl.nv, b->rows, c->stream);
+    if (e != hipSuccess) return zi_hip_fail(e, "entropy kernel launch");
+    return ZI_OK;
+}
+
+extern "C" int32_t zi_apply_mask_rows(zi_ctx *c, const zi_batch *b) {
+    int32_t rc = check_batch(c, b, "zi_apply_mask_rows");
+    if (rc) return rc;
+    if (!b->mask || b->mask_ld < (b->vocab + 31) / 32)
+        return zi_fail(ZI_ERR_INVALID, "zi_apply_mask_rows: mask missing or mask_ld too small");
+    HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+    zi::MaskParams P;
+    P.logits = const_cast<void *>(b->logits);
+    P.ld = b->ld;
+    P.V = b->vocab;
+    P.rows = b->rows;
+    P.dtype = b->dtype;
+    P.mask = b->mask;
+    P.mask_ld = b->mask_ld;
+    hipError_t e = zi::launch_mask(P, c->stream);
+    if (e != hipSuccess) return zi_hip_fail(e, "mask kernel launch");
+    return ZI_OK;
+}

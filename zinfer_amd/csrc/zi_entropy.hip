@@ -1,0 +1,250 @@
+// zi_entropy.hip -- per-row statistics for speculative verification: Shannon
+// entropy (nats) of the T = 1 full-vocabulary softmax, the top-k ids (value
+// desc, id asc) with full-vocabulary probabilities, the lowest-index argmax
+// and argmax == draft acceptance (the compare of src/gen.zig:559).
+//
+// The reference has no entropy: Gen.AdaptiveDraft (src/gen.zig:366-432) is
+// driven by the logit margin.  Definition used here:
+//   M = max x, Z = sum exp(x - M), A = sum exp(x - M) (x - M),
+//   H = ln Z - A / Z,  p_i = exp(x_i - M) / Z.
+// Each thread keeps (ref, S, U) with S = sum exp(x - ref), U = sum exp(x -
+// ref)(x - ref) over its elements; ref moves up only when an element exceeds
+// it by 64 so the f32 sums cannot overflow.  Workgroup and row merges are in
+// f64.
+#include "zi_launch.hpp"
+#include "zi_rowpass.hpp"
+
+namespace zi {
+
+struct SmemEntA {
+    uint64_t ckey[kCapA];
+    float cval[kCapA];
+};
+struct SmemEntB {
+    uint64_t bkey[kMaxG * kCapA];
+    float bval[kMaxG * kCapA];
+    uint64_t tkey[kThreads];
+    float tval[kThreads];
+    uint64_t okey[kThreads];
+    float oval[kThreads];
+};
+union SmemEnt {
+    SmemEntA a;
+    SmemEntB b;
+};
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) v += __shfl_xor(v, m);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max_f(float v) {
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) v = fmaxf(v, __shfl_xor(v, m));
+    return v;
+}
+
+template <typename T, int NV>
+__global__ __launch_bounds__(kThreads) void entropy_kernel(EntropyParams P) {
+    __shared__ SmemEnt sm;
+    __shared__ uint32_t s_bins[256];
+    __shared__ uint32_t s_tau[kWaves];
+    __shared__ int s_dig[2];
+    __shared__ int s_nc, s_flag, s_cnt;
+    __shared__ int s_off[kMaxG + 1];
+    __shared__ float s_wmax[kWaves];
+    __shared__ double s_ws[kWaves], s_wu[kWaves];
+
+    constexpr int VEC = VecTraits<T>::VEC;
+    const RowSource &a = P.src;
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int G = a.G;
+    const int row = blockIdx.x / G;
+    const int g = blockIdx.x - row * G;
+    const int c0 = g * a.CH;
+    const int c1 = min(a.V, c0 + a.CH);
+
+    uint4 raw[NV];
+    uint32_t mw[NV];
+    chunk_load<T, NV>(a, row, c0, c1, raw, mw);
+
+    ChunkRegs<T, NV> cr;
+    float tmax = -INFINITY, ref = -INFINITY, S = 0.0f, U = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        int e0 = c0 + (j * kThreads + tid) * VEC;
+        float v[VEC];
+        unpack<T>(raw[j], v);
+        float m4 = -INFINITY;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+            if (e0 + e >= c1) v[e] = -INFINITY;
+            cr.x[j * VEC + e] = v[e];
+            m4 = fmaxf(m4, v[e]);
+        }
+        tmax = fmaxf(tmax, m4);
+        if (m4 > ref + 64.0f) {
+            if (ref != -INFINITY) {
+                float dl = ref - m4;
+                float sc = __builtin_amdgcn_exp2f(dl * kLog2e);
+                U = (U + dl * S) * sc;
+                S = S * sc;
+            }
+            ref = m4;
+        }
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+            float d = fmaxf(v[e] - ref, -200.0f);
+            float ex = __builtin_amdgcn_exp2f(d * kLog2e);
+            S = S + ex;
+            U = fmaf(ex, d, U);
+        }
+    }
+
+    // workgroup merge of (ref, S, U) in f64
+    float wm = wave_max_f(ref);
+    if (lane == 0) s_wmax[wid] = wm;
+    __syncthreads();
+    float M = s_wmax[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) M = fmaxf(M, s_wmax[w]);
+    double ds = 0.0, du = 0.0;
+    if (ref != -INFINITY && M != -INFINITY) {
+        double sh = (double)ref - (double)M;
+        double sc = exp(sh);
+        ds = (double)S * sc;
+        du = ((double)U + sh * (double)S) * sc;
+    }
+    ds = wave_sum_d(ds);
+    du = wave_sum_d(du);
+    if (lane == 0) {
+        s_ws[wid] = ds;
+        s_wu[wid] = du;
+    }
+
+    const int k = P.k;
+    int nc = chunk_candidates<T, NV>(cr, tmax, c0, c1, k, sm.a.ckey, sm.a.cval, kCapA, &s_nc, s_tau);
+    if (nc > kCapA) nc = chunk_candidates_exact<T, NV>(cr, c0, c1, k, sm.a.ckey, sm.a.cval, &s_nc, s_bins, s_dig);
+    if (tid == 0) {
+        double ts = 0.0, tu = 0.0;
+        for (int w = 0; w < kWaves; ++w) {
+            ts += s_ws[w];
+            tu += s_wu[w];
+        }
+        double *st = P.g_stat + ((int64_t)row * G + g) * 3;
+        st[0] = (double)M;
+        st[1] = ts;
+        st[2] = tu;
+    }
+    if (!publish_and_ticket(sm.a.ckey, sm.a.cval, nc, P.g_key, P.g_val, P.g_cnt, P.tickets, row, g, G, &s_flag))
+        return;
+
+    // ---------------- last workgroup of the row ----------------
+    int N = gather_candidates(P.g_key, P.g_val, P.g_cnt, row, G, sm.b.bkey, sm.b.bval, s_off);
+    const int n = min(k, N);
+    if (n > 0)
+        select_sorted(sm.b.bkey, sm.b.bval, N, n, sm.b.okey, sm.b.oval, sm.b.tkey, sm.b.tval, s_bins, s_dig,
+                      &s_cnt);
+    __shared__ double s_M, s_Z;
+    if (tid == 0) {
+        double Mr = -INFINITY;
+        for (int gg = 0; gg < G; ++gg) Mr = fmax(Mr, P.g_stat[((int64_t)row * G + gg) * 3]);
+        double Z = 0.0, A = 0.0;
+        if (Mr != -INFINITY) {
+            for (int gg = 0; gg < G; ++gg) {
+                const double *st = P.g_stat + ((int64_t)row * G + gg) * 3;
+                if (st[0] == -INFINITY) continue;
+                double sh = st[0] - Mr;
+                double sc = exp(sh);
+                Z += st[1] * sc;
+                A += (st[2] + sh * st[1]) * sc;
+            }
+        }
+        s_M = Mr;
+        s_Z = Z;
+        if (P.entropy) P.entropy[row] = (float)(log(Z) - A / Z);
+        uint32_t am = n > 0 ? ckey_id(sm.b.okey[0]) : 0u;
+        if (P.argmax) P.argmax[row] = am;
+        if (P.accept && P.draft) P.accept[row] = (uint8_t)(am == P.draft[row]);
+    }
+    __syncthreads();
+    if (tid < n) {
+        int64_t o = (int64_t)row * P.out_ld + tid;
+        if (P.ids) P.ids[o] = ckey_id(sm.b.okey[tid]);
+        if (P.probs) P.probs[o] = (float)(exp((double)sm.b.oval[tid] - s_M) / s_Z);
+    }
+}
+
+template <typename T, int NV>
+static hipError_t launch_entropy_t(const EntropyParams &P, int rows, hipStream_t st) {
+    dim3 grid(rows * P.src.G), block(kThreads);
+    hipLaunchKernelGGL((entropy_kernel<T, NV>), grid, block, 0, st, P);
+    return hipGetLastError();
+}
+
+hipError_t launch_entropy(const EntropyParams &P, int dtype, int nv, int rows, hipStream_t st) {
+    if (dtype == 0) {
+        switch (nv) {
+            case 4: return launch_entropy_t<float, 4>(P, rows, st);
+            case 8: return launch_entropy_t<float, 8>(P, rows, st);
+            default: return launch_entropy_t<float, 16>(P, rows, st);
+        }
+    }
+    switch (nv) {
+        case 2: return launch_entropy_t<uint16_t, 2>(P, rows, st);
+        case 4: return launch_entropy_t<uint16_t, 4>(P, rows, st);
+        default: return launch_entropy_t<uint16_t, 8>(P, rows, st);
+    }
+}
+
+// ---------------------------------------------------------------- mask
+// JsonValidator.applyMask (src/grammar.zig:446-479) for a packed mask: clear
+// bit -> -inf, in place.  Vectors whose mask bits are all set are not touched.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void mask_kernel(MaskParams P) {
+    constexpr int VEC = VecTraits<T>::VEC;
+    const int64_t nvr = (P.V + VEC - 1) / VEC;
+    const int64_t total = nvr * P.rows;
+    for (int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x; q < total; q += (int64_t)gridDim.x * kThreads) {
+        int row = (int)(q / nvr);
+        int e0 = (int)(q - (int64_t)row * nvr) * VEC;
+        uint32_t w = P.mask[(int64_t)row * P.mask_ld + (e0 >> 5)];
+        uint32_t bits = (w >> (e0 & 31)) & ((1u << VEC) - 1u);
+        int nvalid = min(VEC, P.V - e0);
+        uint32_t need = (nvalid >= 32) ? 0xFFFFFFFFu : ((1u << nvalid) - 1u);
+        if ((bits & need) == need) continue;
+        T *p = reinterpret_cast<T *>(P.logits) + (int64_t)row * P.ld + e0;
+        uint4 r = *reinterpret_cast<uint4 *>(p);
+        uint32_t *rw = reinterpret_cast<uint32_t *>(&r);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+            if (e < nvalid && !((bits >> e) & 1u)) {
+                if (VEC == 4) {
+                    rw[e] = 0xFF800000u;
+                } else {
+                    uint32_t sh = (e & 1) * 16;
+                    rw[e >> 1] = (rw[e >> 1] & ~(0xFFFFu << sh)) | (0xFF80u << sh);
+                }
+            }
+        }
+        *reinterpret_cast<uint4 *>(p) = r;
+    }
+}
+
+hipError_t launch_mask(const MaskParams &P, hipStream_t st) {
+    const int VEC = P.dtype == 0 ? 4 : 8;
+    int64_t total = (int64_t)((P.V + VEC - 1) / VEC) * P.rows;
+    int64_t blocks = (total + kThreads - 1) / kThreads;
+    if (blocks > 8192) blocks = 8192;
+    if (blocks < 1) blocks = 1;
+    if (P.dtype == 0)
+        hipLaunchKernelGGL(mask_kernel<float>, dim3((unsigned)blocks), dim3(kThreads), 0, st, P);
+    else
+        hipLaunchKernelGGL(mask_kernel<uint16_t>, dim3((unsigned)blocks), dim3(kThreads), 0, st, P);
+    return hipGetLastError();
+}
+
+}  // namespace zi

@@ -1,0 +1,427 @@
+// zi_host.cpp -- host-side mirror of the reference's Zig API around the
+// device path: Sampler (src/sampler.zig:38-286), the DRY edit builder
+// (:104-187), argmaxWithMargin on a host row (:532-614) and
+// Gen.AdaptiveDraft (src/gen.zig:366-432).  Sampling itself always runs on
+// the GPU through zi_sample_rows; this file only keeps the reference's state
+// (RNG, token ring, breakers) and its in-place side effects.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <new>
+
+#include "../../include/zinfer_hip.h"
+#include "zi_internal.hpp"
+#include "zi_launch.hpp"
+
+namespace {
+
+constexpr uint32_t kMaxHistory = 4096;  // src/sampler.zig:31
+constexpr uint32_t kMaxBreakers = 16;   // src/sampler.zig:32
+
+// std.Random.DefaultPrng: xoshiro256++ (Blackman & Vigna) seeded with four
+// splitmix64 outputs; Random.float(f32) builds the float from one 64-bit draw
+// (23 mantissa bits, exponent from the leading-zero count).
+uint64_t splitmix_next(uint64_t &s) {
+    uint64_t z = (s += 0x9e3779b97f4a7c15ULL);
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ULL;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebULL;
+    return z ^ (z >> 31);
+}
+inline uint64_t rotl(uint64_t x, int k) { return (x << k) | (x >> (64 - k)); }
+struct Xoshiro {
+    uint64_t s[4];
+    void seed(uint64_t v) {
+        uint64_t st = v;
+        for (auto &w : s) w = splitmix_next(st);
+    }
+    uint64_t next() {
+        uint64_t r = rotl(s[0] + s[3], 23) + s[0];
+        uint64_t t = s[1] << 17;
+        s[2] ^= s[0];
+        s[3] ^= s[1];
+        s[1] ^= s[2];
+        s[0] ^= s[3];
+        s[2] ^= t;
+        s[3] = rotl(s[3], 45);
+        return r;
+    }
+    float f32() {
+        uint64_t r = next();
+        uint32_t lz = r ? (uint32_t)__builtin_clzll(r) : 64u;
+        if (lz >= 41) {
+            uint64_t r2 = next();
+            lz = 41 + (r2 ? (uint32_t)__builtin_clzll(r2) : 64u);
+            if (lz == 41 + 64) lz += (uint32_t)__builtin_clz((uint32_t)next() | 0x7FFu);
+        }
+        uint32_t bits = ((126u - lz) << 23) | (uint32_t)(r & 0x7FFFFFu);
+        float f;
+        std::memcpy(&f, &bits, 4);
+        return f;
+    }
+};
+
+// src/sampler.zig:91-100 plus the frequency/presence extension, on a host row.
+void host_penalty(float *logits, uint32_t V, const uint32_t *win, uint32_t n, const zi_params &p) {
+    const bool rep = p.repeat_penalty != 1.0f;
+    const bool fp = p.freq_penalty != 0.0f || p.presence_penalty != 0.0f;
+    if (!rep && !fp) return;
+    for (uint32_t i = 0; i < n; ++i) {
+        uint32_t tok = win[i];
+        if (std::find(win, win + i, tok) != win + i) continue;
+        if (tok >= V) continue;
+        float &l = logits[tok];
+        if (rep) l = (l > 0.0f) ? l / p.repeat_penalty : l * p.repeat_penalty;
+        if (fp) {
+            uint32_t cnt = (uint32_t)std::count(win, win + n, tok);
+            float t = (float)cnt * p.freq_penalty;
+            t = t + p.presence_penalty;
+            l = l - t;
+        }
+    }
+}
+
+struct Staging {
+    void *h = nullptr;  // pinned host
+    void *d = nullptr;  // device
+    size_t bytes = 0;
+    ~Staging() {
+        if (h) hipHostFree(h);
+        if (d) hipFree(d);
+    }
+    int32_t ensure(size_t n) {
+        if (n <= bytes) return ZI_OK;
+        if (h) hipHostFree(h);
+        if (d) hipFree(d);
+        h = d = nullptr;
+        bytes = 0;
+        hipError_t e = hipHostMalloc(&h, n, hipHostMallocDefault);
+        if (e == hipSuccess) e = hipMalloc(&d, n);
+        if (e != hipSuccess) return zi_fail(ZI_ERR_OOM, "staging allocation of %zu bytes: %s", n, hipGetErrorString(e));
+        bytes = n;
+        return ZI_OK;
+    }
+};
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+}  // namespace
+
+uint32_t zi_dry_edits_impl(const uint32_t *hist, uint32_t n_hist, const uint32_t *breakers, uint32_t n_breakers,
+                           const zi_params &p, uint32_t *out_ids, float *out_deltas) {
+    // src/sampler.zig:104-187 on a linear history (oldest first): R[k] is the
+    // k-th most recent token.
+    if (p.dry_multiplier == 0.0f || p.dry_base < 1.0f || p.dry_range == 0) return 0;
+    uint32_t L = std::min(n_hist, std::min(p.dry_range, kMaxHistory));
+    if (L <= p.dry_allowed_length) return 0;
+    auto R = [&](uint32_t k) { return hist[n_hist - 1 - k]; };
+    auto is_brk = [&](uint32_t t) { return std::find(breakers, breakers + n_breakers, t) != breakers + n_breakers; };
+    uint32_t rep_limit = L;
+    for (uint32_t k = 0; k < L; ++k)
+        if (is_brk(R(k))) {
+            rep_limit = k;
+            break;
+        }
+    if (rep_limit < p.dry_allowed_length) return 0;
+    static thread_local uint32_t z[kMaxHistory];
+    z[0] = 0;
+    uint32_t l = 0, r = 0;
+    for (uint32_t i = 1; i < L; ++i) {
+        z[i] = (i <= r) ? std::min(r - i + 1, z[i - l]) : 0u;
+        const uint32_t max_z = std::min(L - i, rep_limit);
+        while (z[i] < max_z && R(z[i]) == R(i + z[i])) z[i] += 1;
+        if (i + z[i] > 0 && i + z[i] - 1 > r) {
+            l = i;
+            r = i + z[i] - 1;
+        }
+    }
+    uint32_t n_pen = 0;
+    uint32_t lens[128];
+    for (uint32_t k = 1; k < L; ++k) {
+        const uint32_t rlen = z[k];
+        if (rlen < p.dry_allowed_length) continue;
+        const uint32_t cont = R(k - 1);
+        if (is_brk(cont)) continue;
+        uint32_t pi = 0;
+        while (pi < n_pen && out_ids[pi] != cont) ++pi;
+        if (pi < n_pen) {
+            lens[pi] = std::max(lens[pi], rlen);
+        } else if (n_pen < 128) {
+            out_ids[n_pen] = cont;
+            lens[n_pen] = rlen;
+            ++n_pen;
+        }
+    }
+    const float max_exp = (p.dry_base > 1.0001f) ? 88.0f / std::log(p.dry_base) : 100.0f;
+    for (uint32_t i = 0; i < n_pen; ++i) {
+        float e = std::min((float)(lens[i] - p.dry_allowed_length), max_exp);
+        out_deltas[i] = p.dry_multiplier * std::pow(p.dry_base, e);
+    }
+    return n_pen;
+}
+
+extern "C" uint32_t zi_dry_edits(const uint32_t *hist, uint32_t n_hist, const uint32_t *breakers,
+                                 uint32_t n_breakers, const zi_params *p, uint32_t *out_ids, float *out_deltas) {
+    if (!p || !out_ids || !out_deltas || (n_hist && !hist) || (n_breakers && !breakers)) return 0;
+    return zi_dry_edits_impl(hist, n_hist, breakers, n_breakers, *p, out_ids, out_deltas);
+}
+
+struct zi_sampler {
+    zi_ctx *ctx = nullptr;
+    uint32_t vocab = 0, ld = 0;
+    zi_params p{};
+    Xoshiro rng{};
+    uint32_t history[kMaxHistory];  // ring, src/sampler.zig:44, :87
+    uint64_t n_history = 0;         // accept() also advances the 64-entry ring (:85) in lockstep
+    uint32_t breakers[kMaxBreakers];
+    uint32_t n_breakers = 0;
+    Staging st;
+    // staging layout (bytes)
+    size_t o_logits = 0, o_hist = 0, o_hlen = 0, o_eids = 0, o_edel = 0, o_ecnt = 0, o_u = 0, o_tok = 0,
+           o_margin = 0, o_ndraws = 0, total = 0;
+
+    // Last min(n, W) accepted tokens, oldest first.
+    uint32_t window(uint32_t W, uint32_t *out) const {
+        uint64_t n = std::min<uint64_t>(std::min<uint64_t>(n_history, W), kMaxHistory);
+        for (uint64_t i = 0; i < n; ++i) out[i] = history[(n_history - n + i) & (kMaxHistory - 1)];
+        return (uint32_t)n;
+    }
+};
+
+extern "C" int32_t zi_sampler_init(zi_sampler **out, zi_ctx *ctx, uint32_t vocab, const zi_params *p) {
+    if (!out || !ctx || !p || vocab == 0) return zi_fail(ZI_ERR_INVALID, "zi_sampler_init: bad argument");
+    *out = nullptr;
+    if ((int64_t)vocab > ctx->max_vocab)
+        return zi_fail(ZI_ERR_CAPACITY, "zi_sampler_init: vocab %u > context max_vocab %d", vocab, ctx->max_vocab);
+    zi_sampler *s = new (std::nothrow) zi_sampler();
+    if (!s) return zi_fail(ZI_ERR_OOM, "zi_sampler_init: host allocation");
+    s->ctx = ctx;
+    s->vocab = vocab;
+    s->ld = (vocab + 7u) & ~7u;
+    s->p = *p;
+    s->rng.seed(p->seed);  // :52
+    size_t o = 0;
+    s->o_logits = o;
+    o = align_up(o + (size_t)s->ld * 4, 256);
+    s->o_hist = o;
+    o = align_up(o + zi::kMaxWinHost * 4, 256);
+    s->o_hlen = o;
+    o += 16;
+    s->o_eids = o;
+    o = align_up(o + zi::kMaxEditsHost * 4, 256);
+    s->o_edel = o;
+    o = align_up(o + zi::kMaxEditsHost * 4, 256);
+    s->o_ecnt = o;
+    o += 16;
+    s->o_u = o;
+    o += 16;
+    s->o_tok = o;
+    o += 16;
+    s->o_margin = o;
+    o += 16;
+    s->o_ndraws = o;
+    o += 16;
+    s->total = align_up(o, 256);
+    hipSetDevice(ctx->device);
+    int32_t rc = s->st.ensure(s->total);
+    if (rc) {
+        delete s;
+        return rc;
+    }
+    *out = s;
+    return ZI_OK;
+}
+
+extern "C" void zi_sampler_deinit(zi_sampler *s) { delete s; }
+extern "C" void zi_sampler_reset(zi_sampler *s) {
+    if (s) s->n_history = 0;  // :64-67 clears n_recent and n_history only
+}
+extern "C" void zi_sampler_add_breaker(zi_sampler *s, uint32_t tok) {
+    if (s && s->n_breakers < kMaxBreakers) s->breakers[s->n_breakers++] = tok;  // :69-74
+}
+extern "C" int32_t zi_sampler_is_breaker(const zi_sampler *s, uint32_t tok) {
+    if (!s) return 0;
+    for (uint32_t i = 0; i < s->n_breakers; ++i)
+        if (s->breakers[i] == tok) return 1;
+    return 0;
+}
+extern "C" void zi_sampler_accept(zi_sampler *s, uint32_t tok) {
+    if (!s) return;
+    s->history[s->n_history & (kMaxHistory - 1)] = tok;  // :84-89
+    s->n_history += 1;
+}
+extern "C" void zi_sampler_get_params(const zi_sampler *s, zi_params *p) {
+    if (s && p) *p = s->p;
+}
+extern "C" void zi_sampler_set_params(zi_sampler *s, const zi_params *p) {
+    if (s && p) s->p = *p;
+}
+extern "C" void zi_sampler_seed(zi_sampler *s, uint64_t seed) {
+    if (s) s->rng.seed(seed);
+}
+extern "C" float zi_sampler_rand_f32(zi_sampler *s) { return s ? s->rng.f32() : 0.0f; }
+
+static uint32_t sampler_dry(const zi_sampler *s, uint32_t *ids, float *deltas) {
+    uint32_t lin[kMaxHistory];
+    uint32_t n = s->window(kMaxHistory, lin);
+    return zi_dry_edits_impl(lin, n, s->breakers, s->n_breakers, s->p, ids, deltas);
+}
+
+extern "C" void zi_sampler_apply_dry(const zi_sampler *s, float *logits, uint32_t n) {
+    if (!s || !logits) return;
+    uint32_t ids[128];
+    float d[128];
+    uint32_t m = sampler_dry(s, ids, d);
+    for (uint32_t i = 0; i < m; ++i)
+        if (ids[i] < n) logits[ids[i]] -= d[i];  // :180-185
+}
+
+extern "C" int32_t zi_sampler_sample_with_margin(zi_sampler *s, float *logits, uint32_t n, uint32_t *tok,
+                                                 float *margin) {
+    if (!s || !logits || !tok) return zi_fail(ZI_ERR_INVALID, "zi_sampler_sample_with_margin: bad argument");
+    if (n != s->vocab) return zi_fail(ZI_ERR_INVALID, "zi_sampler_sample_with_margin: n=%u != vocab %u", n, s->vocab);
+    zi_ctx *c = s->ctx;
+    char *h = (char *)s->st.h;
+    char *d = (char *)s->st.d;
+    const zi_params &p = s->p;
+    if (p.penalty_last_n > (uint32_t)zi::kMaxWinHost)
+        return zi_fail(ZI_ERR_UNSUPPORTED, "penalty_last_n %u > %d", p.penalty_last_n, zi::kMaxWinHost);
+
+    std::memcpy(h + s->o_logits, logits, (size_t)n * 4);
+    uint32_t *win = (uint32_t *)(h + s->o_hist);
+    uint32_t nw = s->window(p.penalty_last_n, win);
+    *(int32_t *)(h + s->o_hlen) = (int32_t)nw;
+    uint32_t *eids = (uint32_t *)(h + s->o_eids);
+    float *edel = (float *)(h + s->o_edel);
+    uint32_t ne = sampler_dry(s, eids, edel);
+    *(int32_t *)(h + s->o_ecnt) = (int32_t)ne;
+    Xoshiro peek = s->rng;  // the draws are peeked, then committed per ndraws
+    float *u = (float *)(h + s->o_u);
+    u[0] = peek.f32();
+    u[1] = peek.f32();
+    *(int32_t *)(h + s->o_ndraws) = 0;  // not every path writes ndraws
+
+    hipSetDevice(c->device);
+    hipError_t e = hipMemcpyAsync(d, h, s->o_ndraws + 16, hipMemcpyHostToDevice, c->stream);
+    if (e != hipSuccess) return zi_hip_fail(e, "sampler H2D");
+    zi_batch b;
+    std::memset(&b, 0, sizeof b);
+    b.logits = d + s->o_logits;
+    b.dtype = ZI_F32;
+    b.rows = 1;
+    b.vocab = (int32_t)n;
+    b.ld = (int32_t)s->ld;
+    b.hist = (const uint32_t *)(d + s->o_hist);
+    b.hist_len = (const int32_t *)(d + s->o_hlen);
+    b.hist_ld = zi::kMaxWinHost;
+    if (ne) {
+        b.edit_ids = (const uint32_t *)(d + s->o_eids);
+        b.edit_delta = (const float *)(d + s->o_edel);
+        b.edit_count = (const int32_t *)(d + s->o_ecnt);
+        b.edit_ld = zi::kMaxEditsHost;
+    }
+    zi_sample_out o;
+    std::memset(&o, 0, sizeof o);
+    o.tok = (uint32_t *)(d + s->o_tok);
+    o.margin = (float *)(d + s->o_margin);
+    o.ndraws = (int32_t *)(d + s->o_ndraws);
+    int32_t rc = zi_sample_rows(c, &p, &b, (const float *)(d + s->o_u), &o);
+    if (rc) return rc;
+    e = hipMemcpyAsync(h + s->o_tok, d + s->o_tok, s->o_ndraws + 16 - s->o_tok, hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) return zi_hip_fail(e, "sampler D2H");
+    const int32_t nd = *(int32_t *)(h + s->o_ndraws);
+    for (int32_t i = 0; i < nd; ++i) (void)s->rng.f32();
+    // the reference's in-place side effects: penalty (:191) then DRY (:192)
+    host_penalty(logits, n, win, nw, p);
+    for (uint32_t i = 0; i < ne; ++i)
+        if (eids[i] < n) logits[eids[i]] -= edel[i];
+    *tok = *(uint32_t *)(h + s->o_tok);
+    if (margin) *margin = *(float *)(h + s->o_margin);
+    return ZI_OK;
+}
+
+extern "C" int32_t zi_sampler_sample(zi_sampler *s, float *logits, uint32_t n, uint32_t *tok) {
+    return zi_sampler_sample_with_margin(s, logits, n, tok, nullptr);
+}
+
+extern "C" int32_t zi_argmax_with_margin(zi_ctx *c, const float *logits, uint32_t n, uint32_t *tok, float *margin) {
+    if (!c || !logits || !tok || n == 0) return zi_fail(ZI_ERR_INVALID, "zi_argmax_with_margin: bad argument");
+    if ((int64_t)n > c->max_vocab) return zi_fail(ZI_ERR_CAPACITY, "zi_argmax_with_margin: n > max_vocab");
+    static thread_local Staging st;
+    const uint32_t ld = (n + 7u) & ~7u;
+    const size_t o_out = align_up((size_t)ld * 4, 256);
+    hipSetDevice(c->device);
+    int32_t rc = st.ensure(o_out + 256);
+    if (rc) return rc;
+    std::memcpy(st.h, logits, (size_t)n * 4);
+    hipError_t e = hipMemcpyAsync(st.d, st.h, (size_t)n * 4, hipMemcpyHostToDevice, c->stream);
+    if (e != hipSuccess) return zi_hip_fail(e, "argmax H2D");
+    zi_batch b;
+    std::memset(&b, 0, sizeof b);
+    b.logits = st.d;
+    b.dtype = ZI_F32;
+    b.rows = 1;
+    b.vocab = (int32_t)n;
+    b.ld = (int32_t)ld;
+    char *dout = (char *)st.d + o_out;
+    rc = zi_argmax_rows(c, &b, (uint32_t *)dout, (float *)(dout + 16), nullptr, nullptr);
+    if (rc) return rc;
+    e = hipMemcpyAsync((char *)st.h + o_out, dout, 32, hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) return zi_hip_fail(e, "argmax D2H");
+    *tok = *(uint32_t *)((char *)st.h + o_out);
+    if (margin) *margin = *(float *)((char *)st.h + o_out + 16);
+    return ZI_OK;
+}
+
+// ------------------------------------------------ Gen.AdaptiveDraft mirror
+extern "C" void zi_adaptive_draft_init(zi_adaptive_draft *a, uint64_t max_k) {
+    if (!a) return;
+    a->cur_k = std::min<uint64_t>(max_k, 3);  // gen.zig:374-380
+    a->max_k = max_k;
+    a->min_k = 1;
+    a->consecutive_rejections = 0;
+    a->cooldown_steps = 0;
+    a->last_margin = 2.0f;
+}
+extern "C" void zi_adaptive_draft_record_margin(zi_adaptive_draft *a, float m) {
+    if (a) a->last_margin = m;
+}
+extern "C" uint64_t zi_adaptive_draft_next(zi_adaptive_draft *a) {
+    if (!a) return 0;
+    if (a->cooldown_steps > 0) {  // gen.zig:388-405
+        a->cooldown_steps -= 1;
+        return 0;
+    }
+    uint64_t t = a->cur_k;
+    if (a->last_margin >= 3.0f)
+        t = std::min(a->max_k, std::max<uint64_t>(a->cur_k, 4));
+    else if (a->last_margin >= 1.8f)
+        t = std::min(a->max_k, std::max<uint64_t>(a->cur_k, 2));
+    else if (a->last_margin < 0.9f)
+        t = std::min<uint64_t>(t, 1);
+    return t;
+}
+extern "C" void zi_adaptive_draft_update(zi_adaptive_draft *a, uint64_t accepted, uint64_t drafted,
+                                         int32_t has_margin, float margin) {
+    if (!a) return;
+    if (has_margin) a->last_margin = margin;  // gen.zig:408-431
+    if (drafted == 0) return;
+    if (accepted == drafted) {
+        a->consecutive_rejections = 0;
+        if (a->cur_k < a->max_k) a->cur_k += 1;
+    } else if (accepted > 0) {
+        a->consecutive_rejections = 0;
+        if (accepted * 2 < drafted && a->cur_k > a->min_k) a->cur_k -= 1;
+    } else {
+        a->consecutive_rejections += 1;
+        if (a->cur_k > a->min_k) a->cur_k -= 1;
+        if (a->consecutive_rejections >= 2) {
+            a->cooldown_steps = 2;
+            a->consecutive_rejections = 0;
+            a->cur_k = std::min<uint64_t>(a->max_k, 2);
+        }
+    }
+}

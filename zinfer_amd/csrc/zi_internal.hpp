@@ -1,0 +1,27 @@
+// zi_internal.hpp -- host-side internals shared by the C ABI translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/zinfer_hip.h"
+
+struct zi_ctx {
+    int device = 0;
+    int max_rows = 0;
+    int max_vocab = 0;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    // device scratch (see zi_launch.hpp for layouts)
+    uint64_t *g_key = nullptr;
+    float *g_val = nullptr;
+    int32_t *g_cnt = nullptr;
+    int32_t *tickets = nullptr;
+    double *g_stat = nullptr;
+    uint64_t *g_cls = nullptr;
+    uint32_t *g_raw = nullptr;
+    float *g_top2 = nullptr;
+    float *g_tail = nullptr;
+};
+
+int32_t zi_fail(int32_t code, const char *fmt, ...);
+int32_t zi_hip_fail(hipError_t e, const char *what);

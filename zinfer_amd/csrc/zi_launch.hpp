@@ -1,0 +1,107 @@
+// zi_launch.hpp -- host-visible kernel argument structs and launchers.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace zi {
+
+// Limits shared by the host planner and the kernels.
+constexpr int kThreadsHost = 256;   // threads per workgroup
+constexpr int kMaxGHost = 16;       // chunks per row
+constexpr int kCapAHost = 256;      // candidates one chunk may publish
+constexpr int kMaxChunkElems = 16384;
+constexpr int kMaxVocab = kMaxGHost * kMaxChunkElems;  // 262144
+constexpr int kMaxWinHost = 1024;   // penalty window
+constexpr int kMaxEditsHost = 128;  // sparse edits per row
+constexpr int kMaxTopK = 256;
+constexpr int kMaxEntropyK = 64;
+
+struct Plan {
+    int G, CH, nv;
+};
+Plan plan_rows(int rows, int V, int dtype);
+
+// One batch of logit rows plus the per-row inputs fused into the streaming
+// pass (mask, penalty window, sparse edits).  Device pointers.
+struct RowSource {
+    const void *logits;
+    int64_t ld;
+    int V, G, CH;  // vocab, chunks per row, chunk elements (multiple of 64)
+    const uint32_t *hist;
+    const int32_t *hist_len;
+    int hist_ld, win;  // win = penalty window (penalty_last_n)
+    const uint32_t *mask;
+    int mask_ld;
+    const uint32_t *edit_ids;
+    const float *edit_delta;
+    const int32_t *edit_count;
+    int edit_ld;
+    float rp, freq, pres;
+    int do_rep, do_fp;
+};
+
+struct SampleParams {
+    RowSource src;
+    int k;
+    float temp, top_p, min_p, xtc_p, xtc_thr;
+    int xtc_min_keep;
+    const float *uniforms;
+    uint32_t *tok;
+    float *margin;
+    int32_t *ndraws;
+    int32_t *keep;
+    uint32_t *cand_ids;
+    float *cand_vals;
+    float *probs;
+    int cand_ld;
+    uint64_t *g_key;  // scratch [rows][G][kCapA]
+    float *g_val;
+    int32_t *g_cnt;    // [rows][G]
+    int32_t *tickets;  // [rows], zero between launches
+};
+
+struct ArgmaxParams {
+    RowSource src;
+    uint32_t *tok;
+    float *margin;
+    uint32_t *tok_low;
+    float *margin_true;
+    int32_t *ndraws;     // greedy sampling writes 0 here when given
+    uint64_t *g_cls;     // scratch [rows][G][16] class-max keys (okey << 32 | ~id)
+    uint32_t *g_raw;     // scratch [rows][G][16] raw f32 bits of each class winner
+    float *g_top2;       // scratch [rows][G][2]
+    float *g_tail;       // scratch [rows][16] transformed tail values
+    int32_t *tickets;
+};
+
+struct EntropyParams {
+    RowSource src;
+    int k;
+    const uint32_t *draft;
+    float *entropy;
+    uint32_t *ids;
+    float *probs;
+    int out_ld;
+    uint32_t *argmax;
+    uint8_t *accept;
+    uint64_t *g_key;
+    float *g_val;
+    int32_t *g_cnt;
+    double *g_stat;  // [rows][G][3]: chunk max, sum exp(x - max), sum exp(x - max)(x - max)
+    int32_t *tickets;
+};
+
+struct MaskParams {
+    void *logits;
+    int64_t ld;
+    int V, rows, dtype;
+    const uint32_t *mask;
+    int mask_ld;
+};
+
+hipError_t launch_sample(const SampleParams &P, int dtype, int nv, int rows, hipStream_t st);
+hipError_t launch_argmax(const ArgmaxParams &P, int dtype, int nv, int rows, hipStream_t st);
+hipError_t launch_entropy(const EntropyParams &P, int dtype, int nv, int rows, hipStream_t st);
+hipError_t launch_mask(const MaskParams &P, hipStream_t st);
+
+}  // namespace zi
