@@ -1,0 +1,200 @@
+"""Benchmark: rows/sec and HBM roofline of the batched sampling path.
+
+One step = one zi_sample_rows launch over one batch of BASELINE config 2
+(64 rows x 128256 f32 logits, top_k 50, top_p 0.9, T 0.7, repetition 1.15,
+frequency 0.3, presence 0.5 over 256-token histories), inputs resident in HBM.
+Steps rotate over enough distinct input batches (>= 512 MiB) that the 256 MiB
+Infinity Cache cannot serve them.  The launches are recorded once into a HIP
+graph (as a serving loop would) and replayed, so host submission does not
+limit the measured rate.
+
+Prints ONE JSON line (rank 0).  Only one GPU is used by this build: --gpus N
+with N > 1 exits with a message.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0
+METRIC = "rows/sec + HBM GB/s (% of peak), 64×128256 f32 top-k/top-p sampling"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2048)
+    ap.add_argument("--warmup", type=int, default=128)
+    ap.add_argument("--config", type=int, default=2, help="BASELINE config to run (2 = headline)")
+    ap.add_argument("--rotate-mib", type=int, default=512, help="distinct input bytes cycled through")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample (0 = skip)")
+    ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
+    ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic.md"),
+                    help="rocprofv3 counter summary giving HBM bytes per launch")
+    return ap.parse_args()
+
+
+def read_traffic(path: str, kernel: str, workload: str):
+    """HBM bytes per launch from a committed rocprofv3 --pmc summary line:
+    `traffic <workload> <kernel> <bytes>`."""
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        m = re.match(r"\s*traffic\s+(\S+)\s+(\S+)\s+([0-9.eE+]+)", line)
+        if m and m.group(1) == workload and m.group(2) == kernel:
+            return float(m.group(3))
+    return None
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py: this build runs on one GPU only (the sampling path is row-parallel; "
+              "multi-GPU sharding is described in DESIGN.md and not implemented). Use --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from zinfer_amd.api import Context, SampleResult, params
+    from zinfer_amd.workloads import CONFIGS
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
+    w = CONFIGS[args.config]()
+    rows, V = w.rows, w.vocab
+    if args.config == 4:
+        raise SystemExit("config 4 is benchmarked through tests/; bench.py measures the sampling path")
+    ld = (V + 7) // 8 * 8
+    dt = torch.bfloat16 if w.bf16 else torch.float32
+    elt = 2 if w.bf16 else 4
+    per_set = rows * ld * elt
+    nsets = max(1, (args.rotate_mib * 2**20 + per_set - 1) // per_set)
+    base = torch.zeros((rows, ld), dtype=dt, device=dev)
+    base[:, :V] = torch.from_numpy(w.logits).to(dev).to(dt)
+    sets = []
+    for i in range(nsets):  # distinct bytes per set: cyclic roll keeps the value distribution
+        sets.append(torch.roll(base, shifts=i * 97, dims=1).contiguous() if i else base)
+    hist = torch.from_numpy(w.hist).to(dev) if w.hist is not None else None
+    hist_len = torch.from_numpy(w.hist_len).to(dev) if w.hist is not None else None
+    mask = torch.from_numpy(w.mask).to(dev) if w.mask is not None else None
+    uni = torch.from_numpy(w.uniforms).to(dev)
+    p = params(**w.params)
+    ctx = Context(0, max_rows=max(rows, 64), max_vocab=V)
+    outs = [SampleResult(tok=torch.empty(rows, dtype=torch.int32, device=dev),
+                         margin=torch.empty(rows, dtype=torch.float32, device=dev),
+                         ndraws=torch.empty(rows, dtype=torch.int32, device=dev)) for _ in range(nsets)]
+
+    def launch(i):
+        ctx.sample_rows(p, sets[i], uni, vocab=V, hist=hist, hist_len=hist_len, mask=mask, out=outs[i])
+
+    stream = torch.cuda.Stream(dev)  # default priority
+    with torch.cuda.stream(stream):
+        for i in range(nsets):
+            launch(i)
+        torch.cuda.synchronize()
+        graph = None
+        if not args.no_graph:
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                for i in range(nsets):
+                    launch(i)
+            torch.cuda.synchronize()
+        reps = max(1, args.steps // nsets)
+        steps = reps * nsets
+        wreps = max(1, args.warmup // nsets)
+
+        def run(nrep):
+            for _ in range(nrep):
+                if graph is not None:
+                    graph.replay()
+                else:
+                    for i in range(nsets):
+                        launch(i)
+
+        run(wreps)
+        torch.cuda.synchronize()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ev0.record(stream)
+        run(reps)
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        gpu_ms = ev0.elapsed_time(ev1)
+
+    ms_per_step = gpu_ms / steps
+    rows_per_s = rows / (ms_per_step * 1e-3)
+    nbytes = w.nbytes()
+    achieved = nbytes / (ms_per_step * 1e-3) / 1e9
+    kernel = "sample_kernel"
+    traffic = read_traffic(args.traffic, kernel, w.name)
+
+    # sanity: every replayed batch reproduces the eager result of its set
+    ref = SampleResult(tok=torch.empty(rows, dtype=torch.int32, device=dev),
+                       margin=torch.empty(rows, dtype=torch.float32, device=dev),
+                       ndraws=torch.empty(rows, dtype=torch.int32, device=dev))
+    ctx.sample_rows(p, sets[0], uni, vocab=V, hist=hist, hist_len=hist_len, mask=mask, out=ref)
+    torch.cuda.synchronize()
+    assert torch.equal(ref.tok, outs[0].tok) and torch.equal(ref.margin, outs[0].margin), "replay differs from eager"
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        from oracle import pyoracle
+
+        op = pyoracle.params(**{k: v for k, v in w.params.items()})
+        n_rows_cpu = min(rows, 64)
+        L = np.ascontiguousarray(w.logits[:n_rows_cpu])
+        t1, tok1, _ = pyoracle.bench_sample_rows(op, L, w.hist[:n_rows_cpu] if w.hist is not None else None,
+                                                w.hist_len[:n_rows_cpu] if w.hist is not None else None,
+                                                w.mask[:n_rows_cpu] if w.mask is not None else None,
+                                                w.uniforms[:n_rows_cpu], 1)
+        creps = max(1, int(args.cpu_seconds / max(t1, 1e-6)))
+        tc, tokc, _ = pyoracle.bench_sample_rows(op, L, w.hist[:n_rows_cpu] if w.hist is not None else None,
+                                                w.hist_len[:n_rows_cpu] if w.hist is not None else None,
+                                                w.mask[:n_rows_cpu] if w.mask is not None else None,
+                                                w.uniforms[:n_rows_cpu], creps)
+        gtok = ref.tok.cpu().numpy().astype(np.uint32)[:n_rows_cpu]
+        cpu = {"value": round(n_rows_cpu * creps / tc, 1), "unit": "rows/s", "cores": 1, "kind": "port",
+               "sample": f"{n_rows_cpu} rows of the same batch x {creps} passes ({tc:.1f} s), oracle/oracle.c "
+                         f"(C restatement of src/sampler.zig:91-276), -O3, 1 thread",
+               "tokens_match_gpu": bool(np.array_equal(gtok, tokc))}
+
+    out = {
+        "metric": METRIC,
+        "value": round(rows_per_s, 1),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": wreps * nsets,
+        "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if w.bf16 else "f32",
+        "data": "synthetic, seeded (zinfer_amd/workloads.py): " + w.name,
+        "config": {"workload": w.name, "rows": rows, "vocab": V, **{k: v for k, v in w.params.items()},
+                   "rotating_input_sets": nsets, "input_bytes_cycled": nsets * per_set,
+                   "launch": "eager" if args.no_graph else "hip_graph_replay"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                     "algorithmic_bytes_per_launch": nbytes, "kernel": kernel},
+        "cpu_baseline": cpu,
+        "wall_s": round(wall, 3),
+    }
+    print(json.dumps(out), flush=True)
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

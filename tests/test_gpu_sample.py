@@ -27,6 +27,8 @@ def _rows(rng, kind, rows, V):
         return x
     if kind == "flat":
         return np.full((rows, V), 1.5, np.float32)
+    if kind == "allneginf":  # every candidate -inf: the reference falls back to c[n-1]
+        return np.full((rows, V), -np.inf, np.float32)
     raise ValueError(kind)
 
 
@@ -36,6 +38,8 @@ for i in range(48):
     V = int(_r.choice([1, 2, 7, 15, 16, 17, 100, 255, 256, 1000, 4099, 16385, 32000, 70001, 131072]))
     rows = int(_r.choice([1, 3, 9]))
     kind = str(_r.choice(["normal", "t3", "ints", "neginf", "flat"]))
+    if i % 16 == 15:
+        kind = "allneginf"
     top_k = int(_r.choice([1, 2, 5, 40, 64, 200, 256]))
     if V <= 256 and _r.random() < 0.3:
         top_k = 0

@@ -30,11 +30,20 @@ __device__ __forceinline__ void ref_step(float v, uint32_t id, float &best, floa
     }
 }
 
-template <typename T, int NV>
+template <bool P>
+struct ArgPenLds {
+    PenTable pen;
+    FlagList fl;
+};
+template <>
+struct ArgPenLds<false> {};
+
+template <typename T, int NV, bool HAS_MASK, bool HAS_PEN>
 __global__ __launch_bounds__(kThreads) void argmax_kernel(ArgmaxParams P) {
-    __shared__ PenTable pen;
+    __shared__ ArgPenLds<HAS_PEN> pl;
     __shared__ unsigned long long s_ck[16];
     __shared__ uint32_t s_raw[16];
+    __shared__ float s_tail[16];
     __shared__ float s_t1[kWaves], s_t2[kWaves];
     __shared__ int s_flag;
 
@@ -49,26 +58,26 @@ __global__ __launch_bounds__(kThreads) void argmax_kernel(ArgmaxParams P) {
     const int body_end = a.V & ~15;
 
     RowPen rp = row_pen(a, row);
-    PenRegs pr;
-    if (rp.any) pen_fetch(rp, pr);
-    uint4 raw[NV];
-    uint32_t mw[NV];
-    chunk_load<T, NV>(a, row, c0, c1, raw, mw);
+    PenTable *pen = nullptr;
+    FlagList *fl = nullptr;
+    if constexpr (HAS_PEN) {
+        pen = &pl.pen;
+        fl = &pl.fl;
+    }
     if (tid < 16) {
         s_ck[tid] = 0ull;
         s_raw[tid] = 0x7FC00000u;
+        s_tail[tid] = __builtin_nanf("");
     }
-    if (rp.any) pen_build(pen, rp, pr, c0, c1);
     ChunkRegs<T, NV> cr;
-    chunk_transform<T, NV>(a, pen, rp, c0, c1, raw, mw, cr);
-    __syncthreads();  // s_ck / s_raw initialised before any wave's atomics
+    chunk_stream<T, NV, HAS_MASK, HAS_PEN>(a, row, c0, c1, cr, pen, fl, rp);
+    __syncthreads();  // s_* initialised, diverted list complete
 
     // per-thread class records (thread t only meets classes (t*VEC + e) & 15)
     uint64_t ck[VEC];
     float t1 = -INFINITY, t2 = -INFINITY;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) ck[e] = 0ull;
-    float *g_tail = P.g_tail + (int64_t)row * 16;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         int e0 = c0 + (j * kThreads + tid) * VEC;
@@ -76,16 +85,27 @@ __global__ __launch_bounds__(kThreads) void argmax_kernel(ArgmaxParams P) {
         for (int e = 0; e < VEC; ++e) {
             int id = e0 + e;
             float x = cr.x[j * VEC + e];
-            if (id < c1) {
-                if (id >= body_end) g_tail[id - body_end] = x;
-                if (x == x) {
-                    if (id < body_end) {
-                        uint64_t k = ckey(x, (uint32_t)id);
-                        ck[e] = k > ck[e] ? k : ck[e];
-                    }
-                    top2_merge(t1, t2, x, -INFINITY);
+            if (x == x) {  // NaN: past the chunk, diverted, or a NaN input
+                if (id < body_end) {
+                    uint64_t k = ckey(x, (uint32_t)id);
+                    ck[e] = k > ck[e] ? k : ck[e];
+                } else {
+                    s_tail[id - body_end] = x;
                 }
+                top2_merge(t1, t2, x, -INFINITY);
             }
+        }
+    }
+    // diverted (penalized) elements: one per thread
+    int nf = 0;
+    if constexpr (HAS_PEN) nf = fl->n;
+    for (int i = tid; i < nf; i += kThreads) {
+        uint32_t id;
+        float v = flag_value(a, *pen, *fl, rp, i, id);
+        if (v == v) {
+            if ((int)id < body_end) atomicMax(&s_ck[id & 15], (unsigned long long)ckey(v, id));
+            else s_tail[id - body_end] = v;
+            top2_merge(t1, t2, v, -INFINITY);
         }
     }
     // reduce records over lanes sharing the same classes, top-2 over the wave
@@ -119,32 +139,33 @@ __global__ __launch_bounds__(kThreads) void argmax_kernel(ArgmaxParams P) {
         for (int e = 0; e < VEC; ++e) {
             int id = e0 + e;
             float x = cr.x[j * VEC + e];
-            if (id < c1 && id < body_end && x == x && ckey(x, (uint32_t)id) == s_ck[cls0 + e])
+            if (id < body_end && x == x && ckey(x, (uint32_t)id) == s_ck[cls0 + e])
                 s_raw[cls0 + e] = __float_as_uint(x);
         }
+    }
+    for (int i = tid; i < nf; i += kThreads) {
+        uint32_t id;
+        float v = flag_value(a, *pen, *fl, rp, i, id);
+        if ((int)id < body_end && v == v && ckey(v, id) == s_ck[id & 15]) s_raw[id & 15] = __float_as_uint(v);
     }
     __syncthreads();
     const int64_t rg = (int64_t)row * G + g;
     if (tid < 16) {
-        P.g_cls[rg * 16 + tid] = s_ck[tid];
-        P.g_raw[rg * 16 + tid] = s_raw[tid];
+        st_agent(&P.g_cls[rg * 16 + tid], (uint64_t)s_ck[tid]);
+        st_agent(&P.g_raw[rg * 16 + tid], s_raw[tid]);
+        if (body_end + tid < a.V && body_end + tid >= c0 && body_end + tid < c1)
+            st_agent(&P.g_tail[(int64_t)row * 16 + tid], s_tail[tid]);
     }
     if (tid == 0) {
         float a1 = s_t1[0], a2 = s_t2[0];
         for (int w = 1; w < kWaves; ++w) top2_merge(a1, a2, s_t1[w], s_t2[w]);
-        P.g_top2[rg * 2] = a1;
-        P.g_top2[rg * 2 + 1] = a2;
+        st_agent(&P.g_top2[rg * 2], a1);
+        st_agent(&P.g_top2[rg * 2 + 1], a2);
     }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) s_flag = (atomicAdd(&P.tickets[row], 1) == G - 1);
-    __syncthreads();
-    if (!s_flag) return;
-    __threadfence();
+    if (!row_ticket(P.tickets, row, G, &s_flag)) return;
     if (tid != 0) return;
 
     // ---------------- the last workgroup of the row: lane 0 ----------------
-    P.tickets[row] = 0;
     const int V = a.V;
     uint64_t cls[16];
     uint32_t craw[16];
@@ -158,16 +179,18 @@ __global__ __launch_bounds__(kThreads) void argmax_kernel(ArgmaxParams P) {
         const int64_t r2 = (int64_t)row * G + gg;
 #pragma unroll
         for (int c = 0; c < 16; ++c) {
-            uint64_t k = P.g_cls[r2 * 16 + c];
+            uint64_t k = ld_agent(&P.g_cls[r2 * 16 + c]);
+            uint32_t rw = ld_agent(&P.g_raw[r2 * 16 + c]);
             if (k > cls[c]) {
                 cls[c] = k;
-                craw[c] = P.g_raw[r2 * 16 + c];
+                craw[c] = rw;
             }
         }
-        top2_merge(a1, a2, P.g_top2[r2 * 2], P.g_top2[r2 * 2 + 1]);
+        top2_merge(a1, a2, ld_agent(&P.g_top2[r2 * 2]), ld_agent(&P.g_top2[r2 * 2 + 1]));
     }
     const int nt = V - body_end;
-    const float *tl = P.g_tail + (int64_t)row * 16;
+    float *tl = s_tail;  // reused: this workgroup's own tail copy is no longer needed
+    for (int i = 0; i < nt; ++i) tl[i] = ld_agent(&P.g_tail[(int64_t)row * 16 + i]);
 
     uint32_t tok = 0;
     float margin = 10.0f;
@@ -220,25 +243,35 @@ __global__ __launch_bounds__(kThreads) void argmax_kernel(ArgmaxParams P) {
     if (P.margin_true) P.margin_true[row] = (V >= 2 && a2 > -INFINITY) ? a1 - a2 : 10.0f;
 }
 
-template <typename T, int NV>
+template <typename T, int NV, bool M, bool PN>
 static hipError_t launch_argmax_t(const ArgmaxParams &P, int rows, hipStream_t st) {
     dim3 grid(rows * P.src.G), block(kThreads);
-    hipLaunchKernelGGL((argmax_kernel<T, NV>), grid, block, 0, st, P);
+    hipLaunchKernelGGL((argmax_kernel<T, NV, M, PN>), grid, block, 0, st, P);
     return hipGetLastError();
+}
+
+template <typename T, int NV>
+static hipError_t launch_argmax_nv(const ArgmaxParams &P, int rows, hipStream_t st) {
+    const bool m = P.src.mask != nullptr;
+    const bool p = (P.src.hist != nullptr) || (P.src.edit_ids != nullptr);
+    if (m && p) return launch_argmax_t<T, NV, true, true>(P, rows, st);
+    if (m) return launch_argmax_t<T, NV, true, false>(P, rows, st);
+    if (p) return launch_argmax_t<T, NV, false, true>(P, rows, st);
+    return launch_argmax_t<T, NV, false, false>(P, rows, st);
 }
 
 hipError_t launch_argmax(const ArgmaxParams &P, int dtype, int nv, int rows, hipStream_t st) {
     if (dtype == 0) {
         switch (nv) {
-            case 4: return launch_argmax_t<float, 4>(P, rows, st);
-            case 8: return launch_argmax_t<float, 8>(P, rows, st);
-            default: return launch_argmax_t<float, 16>(P, rows, st);
+            case 4: return launch_argmax_nv<float, 4>(P, rows, st);
+            case 8: return launch_argmax_nv<float, 8>(P, rows, st);
+            default: return launch_argmax_nv<float, 16>(P, rows, st);
         }
     }
     switch (nv) {
-        case 2: return launch_argmax_t<uint16_t, 2>(P, rows, st);
-        case 4: return launch_argmax_t<uint16_t, 4>(P, rows, st);
-        default: return launch_argmax_t<uint16_t, 8>(P, rows, st);
+        case 2: return launch_argmax_nv<uint16_t, 2>(P, rows, st);
+        case 4: return launch_argmax_nv<uint16_t, 4>(P, rows, st);
+        default: return launch_argmax_nv<uint16_t, 8>(P, rows, st);
     }
 }
 

@@ -16,21 +16,14 @@
 
 namespace zi {
 
-struct SmemEntA {
-    uint64_t ckey[kCapA];
-    float cval[kCapA];
+template <typename T, int NV>
+struct EntStageA {
+    SelectLds<T, NV> sel;
 };
-struct SmemEntB {
-    uint64_t bkey[kMaxG * kCapA];
-    float bval[kMaxG * kCapA];
-    uint64_t tkey[kThreads];
-    float tval[kThreads];
+struct EntStageB {
+    MergeLds ml;
     uint64_t okey[kThreads];
     float oval[kThreads];
-};
-union SmemEnt {
-    SmemEntA a;
-    SmemEntB b;
 };
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -47,18 +40,45 @@ __device__ __forceinline__ float wave_max_f(float v) {
     return v;
 }
 
+// Per-thread running (ref, S, U), updated per vector as its load lands.
+struct EntHook {
+    float *ref, *S, *U;
+    template <int VEC>
+    __device__ void operator()(int, const float (&v)[VEC], float m4) const {
+        if (m4 > *ref + 64.0f) {  // also the first finite value (ref = -inf)
+            if (*ref != -INFINITY) {
+                float dl = *ref - m4;
+                float sc = __builtin_amdgcn_exp2f(dl * kLog2e);
+                *U = (*U + dl * *S) * sc;
+                *S = *S * sc;
+            }
+            *ref = m4;
+        }
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+            float d = fmaxf(v[e] - *ref, -200.0f);  // -inf and NaN contribute 0
+            float ex = __builtin_amdgcn_exp2f(d * kLog2e);
+            *S = *S + ex;
+            *U = fmaf(ex, d, *U);
+        }
+    }
+};
+
 template <typename T, int NV>
 __global__ __launch_bounds__(kThreads) void entropy_kernel(EntropyParams P) {
-    __shared__ SmemEnt sm;
+    __shared__ union {
+        EntStageA<T, NV> a;
+        EntStageB b;
+    } sm;
     __shared__ uint32_t s_bins[256];
     __shared__ uint32_t s_tau[kWaves];
+    __shared__ int s_wcnt[kWaves];
     __shared__ int s_dig[2];
-    __shared__ int s_nc, s_flag, s_cnt;
-    __shared__ int s_off[kMaxG + 1];
+    __shared__ int s_n, s_flag;
     __shared__ float s_wmax[kWaves];
     __shared__ double s_ws[kWaves], s_wu[kWaves];
+    __shared__ double s_M, s_Z;
 
-    constexpr int VEC = VecTraits<T>::VEC;
     const RowSource &a = P.src;
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int G = a.G;
@@ -66,43 +86,13 @@ __global__ __launch_bounds__(kThreads) void entropy_kernel(EntropyParams P) {
     const int g = blockIdx.x - row * G;
     const int c0 = g * a.CH;
     const int c1 = min(a.V, c0 + a.CH);
+    const int k = P.k;
 
-    uint4 raw[NV];
-    uint32_t mw[NV];
-    chunk_load<T, NV>(a, row, c0, c1, raw, mw);
-
+    RowPen rp{};
     ChunkRegs<T, NV> cr;
-    float tmax = -INFINITY, ref = -INFINITY, S = 0.0f, U = 0.0f;
-#pragma unroll
-    for (int j = 0; j < NV; ++j) {
-        int e0 = c0 + (j * kThreads + tid) * VEC;
-        float v[VEC];
-        unpack<T>(raw[j], v);
-        float m4 = -INFINITY;
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-            if (e0 + e >= c1) v[e] = -INFINITY;
-            cr.x[j * VEC + e] = v[e];
-            m4 = fmaxf(m4, v[e]);
-        }
-        tmax = fmaxf(tmax, m4);
-        if (m4 > ref + 64.0f) {
-            if (ref != -INFINITY) {
-                float dl = ref - m4;
-                float sc = __builtin_amdgcn_exp2f(dl * kLog2e);
-                U = (U + dl * S) * sc;
-                S = S * sc;
-            }
-            ref = m4;
-        }
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-            float d = fmaxf(v[e] - ref, -200.0f);
-            float ex = __builtin_amdgcn_exp2f(d * kLog2e);
-            S = S + ex;
-            U = fmaf(ex, d, U);
-        }
-    }
+    float ref = -INFINITY, S = 0.0f, U = 0.0f;
+    float tmax = chunk_stream<T, NV, false, false, EntHook>(a, row, c0, c1, cr, nullptr, nullptr, rp,
+                                                            EntHook{&ref, &S, &U});
 
     // workgroup merge of (ref, S, U) in f64
     float wm = wave_max_f(ref);
@@ -125,42 +115,37 @@ __global__ __launch_bounds__(kThreads) void entropy_kernel(EntropyParams P) {
         s_wu[wid] = du;
     }
 
-    const int k = P.k;
-    int nc = chunk_candidates<T, NV>(cr, tmax, c0, c1, k, sm.a.ckey, sm.a.cval, kCapA, &s_nc, s_tau);
-    if (nc > kCapA) nc = chunk_candidates_exact<T, NV>(cr, c0, c1, k, sm.a.ckey, sm.a.cval, &s_nc, s_bins, s_dig);
+    const int64_t rg = (int64_t)row * G + g;
+    ChunkOut out{P.g_key + rg * kCapA, P.g_val + rg * kCapA, P.g_cnt + rg};
+    chunk_select_publish<T, NV, false>(a, rp, cr, tmax, c0, k, sm.a.sel, nullptr, nullptr, s_tau, s_wcnt, &s_n,
+                                       s_bins, s_dig, out);
     if (tid == 0) {
         double ts = 0.0, tu = 0.0;
         for (int w = 0; w < kWaves; ++w) {
             ts += s_ws[w];
             tu += s_wu[w];
         }
-        double *st = P.g_stat + ((int64_t)row * G + g) * 3;
-        st[0] = (double)M;
-        st[1] = ts;
-        st[2] = tu;
+        st_agent(&P.g_stat[rg * 3], (double)M);
+        st_agent(&P.g_stat[rg * 3 + 1], ts);
+        st_agent(&P.g_stat[rg * 3 + 2], tu);
     }
-    if (!publish_and_ticket(sm.a.ckey, sm.a.cval, nc, P.g_key, P.g_val, P.g_cnt, P.tickets, row, g, G, &s_flag))
-        return;
+    if (!row_ticket(P.tickets, row, G, &s_flag)) return;
 
     // ---------------- last workgroup of the row ----------------
-    int N = gather_candidates(P.g_key, P.g_val, P.g_cnt, row, G, sm.b.bkey, sm.b.bval, s_off);
-    const int n = min(k, N);
-    if (n > 0)
-        select_sorted(sm.b.bkey, sm.b.bval, N, n, sm.b.okey, sm.b.oval, sm.b.tkey, sm.b.tval, s_bins, s_dig,
-                      &s_cnt);
-    __shared__ double s_M, s_Z;
+    const int n = row_merge(P.g_key, P.g_val, P.g_cnt, row, G, k, sm.b.ml, sm.b.okey, sm.b.oval);
     if (tid == 0) {
+        const double *gs = P.g_stat + (int64_t)row * G * 3;
         double Mr = -INFINITY;
-        for (int gg = 0; gg < G; ++gg) Mr = fmax(Mr, P.g_stat[((int64_t)row * G + gg) * 3]);
+        for (int gg = 0; gg < G; ++gg) Mr = fmax(Mr, ld_agent(&gs[gg * 3]));
         double Z = 0.0, A = 0.0;
         if (Mr != -INFINITY) {
             for (int gg = 0; gg < G; ++gg) {
-                const double *st = P.g_stat + ((int64_t)row * G + gg) * 3;
-                if (st[0] == -INFINITY) continue;
-                double sh = st[0] - Mr;
+                const double m = ld_agent(&gs[gg * 3]), sg = ld_agent(&gs[gg * 3 + 1]), ug = ld_agent(&gs[gg * 3 + 2]);
+                if (m == -INFINITY) continue;
+                double sh = m - Mr;
                 double sc = exp(sh);
-                Z += st[1] * sc;
-                A += (st[2] + sh * st[1]) * sc;
+                Z += sg * sc;
+                A += (ug + sh * sg) * sc;
             }
         }
         s_M = Mr;

@@ -9,6 +9,12 @@
 //           window once: l > 0 ? l / rp : l * rp), then the frequency/presence
 //           extension l -= fl(fl(count * freq) + presence).
 //   edits : the DRY subtraction logits[tok] -= penalty, src/sampler.zig:184.
+//
+// Hot-loop design: every load is issued unconditionally (addresses clamped
+// into the chunk) so the compiler waits per load and the transform overlaps
+// the stream; lanes past the chunk end become NaN (never selected, ignored by
+// fmaxf); penalized ids are rare, so they are pulled out of the stream into an
+// LDS side list and penalized after it.
 #pragma once
 #include "zi_common.hpp"
 #include "zi_launch.hpp"
@@ -19,12 +25,43 @@ constexpr int kMaxCH = kMaxChunkElems;  // max chunk elements (256 threads x 64)
 constexpr int kHashMax = 2048;          // LDS hash slots (window + edits <= 1152 ids)
 constexpr int kMaxWin = kMaxWinHost;    // max penalty window
 constexpr int kMaxEdits = kMaxEditsHost;
-constexpr int kCapA = kCapAHost;        // candidates one chunk may publish
+constexpr int kCapA = kCapAHost;        // published candidates per chunk (>= top-k)
 constexpr int kMaxG = kMaxGHost;        // max chunks per row (V <= 262144)
+constexpr int kWaveCap = 256;           // stage-A candidates one wave may hold
+constexpr int kFlagMax = kMaxWin + kMaxEdits;
 static_assert(kThreads == kThreadsHost, "workgroup size");
 
-// RowSource is declared in zi_launch.hpp (host-visible).
+// ------------------------------------------------ cross-workgroup handoff
+// Chunk results travel through device scratch with agent-scope relaxed
+// atomics (sc1: coherent across the XCDs' L2s) and one vmcnt(0) wait before
+// the row ticket, instead of whole-L2 writeback / invalidate fences.
+template <class T>
+__device__ __forceinline__ void st_agent(T *p, T v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class T>
+__device__ __forceinline__ T ld_agent(const T *p) {
+    return __hip_atomic_load(const_cast<T *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
 
+// Returns true in exactly one workgroup of the row (the last to finish);
+// every thread's agent-scope stores are performed before the ticket moves.
+// The last workgroup re-arms the ticket for the next launch.
+__device__ __forceinline__ bool row_ticket(int32_t *tickets, int row, int G, int *s_flag) {
+    wait_vmem();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int old = __hip_atomic_fetch_add(&tickets[row], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        bool last = old == G - 1;
+        if (last) st_agent(&tickets[row], 0);
+        *s_flag = last;
+    }
+    __syncthreads();
+    return *s_flag != 0;
+}
+
+// --------------------------------------------------------- penalty table
 struct PenTable {
     uint32_t bits[kMaxCH / 32];
     uint32_t key[kHashMax];
@@ -92,8 +129,6 @@ __device__ __forceinline__ RowPen row_pen(const RowSource &a, int row) {
     return r;
 }
 
-// Fetches this thread's share of the window and edits (issued before the
-// logit loads so that waiting for them does not wait for the row).
 struct PenRegs {
     uint32_t w[kMaxWin / kThreads];
     uint32_t e;
@@ -116,7 +151,8 @@ __device__ __forceinline__ void pen_fetch(const RowPen &rp, PenRegs &pr) {
 __device__ __forceinline__ void pen_build(PenTable &t, const RowPen &rp, const PenRegs &pr, int c0, int c1) {
     const int tid = threadIdx.x;
     const int hs = 1 << rp.hs_log2;
-    for (int i = tid; i < kMaxCH / 32; i += kThreads) t.bits[i] = 0u;
+    const int nbw = (c1 - c0 + 31) >> 5;
+    for (int i = tid; i < nbw; i += kThreads) t.bits[i] = 0u;
     for (int i = tid; i < hs; i += kThreads) {
         t.key[i] = 0u;
         t.cnt[i] = 0u;
@@ -152,109 +188,190 @@ __device__ __forceinline__ float pen_apply(float v, uint32_t cnt, float delta, c
     return v - delta;  // exact identity when delta == 0
 }
 
-// One thread's chunk share: NV vectors of VEC elements, transformed to the
-// penalized f32 values the reference samples from.
+// ------------------------------------------------------------ the stream
 template <typename T, int NV>
 struct ChunkRegs {
     static constexpr int VEC = VecTraits<T>::VEC;
-    static constexpr int N = NV * VEC;
-    float x[N];
+    float x[NV * VEC];
+    float m4[NV];  // per-vector maxima (NaN lanes ignored)
+    float m1;      // lane max (first occurrence), its id, and the lane's
+    uint32_t id1;  // second largest value (multiset), all kept as loads land
+    float m2;
 };
 
-template <typename T, int NV>
-__device__ __forceinline__ void chunk_load(const RowSource &a, int row, int c0, int c1, uint4 (&raw)[NV],
-                                           uint32_t (&mw)[NV]) {
+struct FlagList {  // penalized / edited elements diverted from the stream
+    uint32_t id[kFlagMax];
+    float x[kFlagMax];
+    int n;
+};
+
+// Streams the chunk [c0, c1) of `row` into registers with the mask applied
+// and penalized ids diverted into `fl` (their register copies become NaN).
+// Returns the thread max (-inf if the thread holds no selectable value);
+// hook(j, v, max) sees each transformed vector as soon as its load lands.
+// HAS_PEN needs PenTable `t` and FlagList `fl` in LDS and contains barriers.
+struct NoHook {
+    template <int VEC>
+    __device__ void operator()(int, const float (&)[VEC], float) const {}
+};
+
+template <typename T, int NV, bool HAS_MASK, bool HAS_PEN, class Hook = NoHook>
+__device__ __forceinline__ float chunk_stream(const RowSource &a, int row, int c0, int c1, ChunkRegs<T, NV> &cr,
+                                              PenTable *t, FlagList *fl, const RowPen &rp, Hook hook = Hook()) {
     constexpr int VEC = VecTraits<T>::VEC;
     const int tid = threadIdx.x;
-    const T *base = reinterpret_cast<const T *>(a.logits) + (int64_t)row * a.ld;
-    const uint32_t *mrow = a.mask ? a.mask + (int64_t)row * a.mask_ld : nullptr;
+    const int nvec = (c1 - c0 + VEC - 1) / VEC;
+    const T *base = reinterpret_cast<const T *>(a.logits) + (int64_t)row * a.ld + c0;
+    const uint32_t *mrow = HAS_MASK ? a.mask + (int64_t)row * a.mask_ld : nullptr;
+
+    PenRegs pr;
+    if (HAS_PEN) pen_fetch(rp, pr);  // issued first: waiting for these does not wait for the row
+    uint4 raw[NV];
+    uint32_t mw[NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-        int e0 = c0 + (j * kThreads + tid) * VEC;
-        if (e0 < c1) {
-            raw[j] = *reinterpret_cast<const uint4 *>(base + e0);
-            mw[j] = mrow ? mrow[e0 >> 5] : 0xFFFFFFFFu;
-        } else {
-            raw[j] = make_uint4(0u, 0u, 0u, 0u);
-            mw[j] = 0u;
+        int q = min(j * kThreads + tid, nvec - 1);
+        raw[j] = *reinterpret_cast<const uint4 *>(base + q * VEC);
+        if (HAS_MASK) mw[j] = mrow[(c0 + q * VEC) >> 5];
+    }
+    uint32_t pw[NV];
+    if (HAS_PEN) {
+        if (tid == 0) fl->n = 0;
+        pen_build(*t, rp, pr, c0, c1);
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            int q = min(j * kThreads + tid, nvec - 1);
+            pw[j] = t->bits[(q * VEC) >> 5];
         }
     }
-}
-
-// Unpacks, applies mask / penalty / edits and returns the thread max over its
-// valid elements (-inf if none; NaNs never win fmaxf).
-template <typename T, int NV>
-__device__ __forceinline__ float chunk_transform(const RowSource &a, const PenTable &t, const RowPen &rp, int c0,
-                                                 int c1, const uint4 (&raw)[NV], const uint32_t (&mw)[NV],
-                                                 ChunkRegs<T, NV> &cr) {
-    constexpr int VEC = VecTraits<T>::VEC;
-    const int tid = threadIdx.x;
     float tmax = -INFINITY;
+    cr.m1 = -INFINITY;
+    cr.m2 = -INFINITY;
+    cr.id1 = 0xFFFFFFFFu;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-        int e0 = c0 + (j * kThreads + tid) * VEC;
+        const int q = j * kThreads + tid;
+        const int id0 = c0 + q * VEC;
         float v[VEC];
         unpack<T>(raw[j], v);
-        uint32_t mbits = (mw[j] >> (e0 & 31)) & ((1u << VEC) - 1u);
-        uint32_t pbits = 0u;
-        if (rp.any && e0 < c1) pbits = (t.bits[(e0 - c0) >> 5] >> ((e0 - c0) & 31)) & ((1u << VEC) - 1u);
+        if (HAS_MASK) {
+            uint32_t mb = mw[j] >> (id0 & 31);
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) v[e] = ((mb >> e) & 1u) ? v[e] : -INFINITY;
+        }
+        if (HAS_PEN) {
+            uint32_t pb = (pw[j] >> ((q * VEC) & 31)) & ((1u << VEC) - 1u);
+            if (pb && id0 < c1) {
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) {
+                    if ((pb >> e) & 1u) {
+                        int s = atomicAdd(&fl->n, 1);
+                        fl->id[s] = (uint32_t)(id0 + e);
+                        fl->x[s] = v[e];
+                        v[e] = __builtin_nanf("");
+                    }
+                }
+            }
+        }
+        const int lim = c1 - id0;
+        if (lim < VEC) {
+#pragma unroll
+            for (int e = 0; e < VEC; ++e)
+                if (e >= lim) v[e] = __builtin_nanf("");
+        }
+        float m = v[0];
+#pragma unroll
+        for (int e = 1; e < VEC; ++e) m = fmaxf(m, v[e]);
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
-            float x = v[e];
-            if (!((mbits >> e) & 1u)) x = -INFINITY;
-            if ((pbits >> e) & 1u) {
-                int h = pen_find(t, (uint32_t)(e0 + e), rp.hs_log2);
-                x = pen_apply(x, t.cnt[h], t.delta[h], a);
-            }
-            bool valid = e0 + e < c1;
-            cr.x[j * VEC + e] = x;
-            if (valid) tmax = fmaxf(tmax, x);
+            cr.x[j * VEC + e] = v[e];
+            const bool gt = v[e] > cr.m1;  // strict: the first (lowest id) maximum stays
+            cr.m2 = gt ? cr.m1 : fmaxf(cr.m2, v[e]);
+            cr.id1 = gt ? (uint32_t)(id0 + e) : cr.id1;
+            cr.m1 = gt ? v[e] : cr.m1;
         }
+        cr.m4[j] = m;
+        tmax = fmaxf(tmax, m);
+        hook.template operator()<VEC>(j, v, m);
     }
     return tmax;
 }
 
-// Stage A: publish a superset of this chunk's top-k (value desc, id asc) to
-// the LDS candidate list.  Threshold: each wave finds the ceil(k/4)-th largest
-// of its lanes' maxima; the minimum over the 4 waves is <= the chunk's k-th
-// largest element (each wave owns ceil(k/4) distinct elements at or above
-// it), so every element of the chunk's top-k passes.  Returns the number of
-// candidates found (which may exceed cap; then the list is incomplete).
-template <typename T, int NV>
-__device__ __forceinline__ int chunk_candidates(const ChunkRegs<T, NV> &cr, float tmax, int c0, int c1, int k,
-                                                uint64_t *s_key, float *s_val, int cap, int *s_nc,
-                                                uint32_t *s_tau) {
-    constexpr int VEC = VecTraits<T>::VEC;
+// Penalized value of diverted entry i (call after a barrier that follows
+// chunk_stream).
+__device__ __forceinline__ float flag_value(const RowSource &a, const PenTable &t, const FlagList &fl,
+                                            const RowPen &rp, int i, uint32_t &id) {
+    id = fl.id[i];
+    int h = pen_find(t, id, rp.hs_log2);
+    return pen_apply(fl.x[i], t.cnt[h], t.delta[h], a);
+}
+
+// --------------------------------------------------------- stage A select
+// Candidate threshold: each wave takes the ceil(k/4)-th largest of its lanes'
+// maxima; the minimum over the 4 waves is <= the k-th largest value the
+// stream kept (each wave owns ceil(k/4) distinct values at or above it), so
+// every element of the chunk's top-k that the stream kept passes, and every
+// diverted (penalized) element above it is added separately.  Returns tau
+// (-inf when some wave has too few values).
+__device__ __forceinline__ float chunk_tau(float tmax, int k, uint32_t *s_tau) {
     const int tid = threadIdx.x;
-    const int wid = tid >> 6;
-    bool present = c0 + tid * VEC < c1;
-    uint32_t mkey = present ? okey(tmax) : 0u;
+    uint32_t mkey = (tmax == tmax) ? okey(tmax) : 0u;
     int r = (k + kWaves - 1) / kWaves;
     uint32_t tw = wave_kth_largest(mkey, r);
-    if ((tid & 63) == 0) s_tau[wid] = tw;
-    if (tid == 0) *s_nc = 0;
+    if ((tid & 63) == 0) s_tau[tid >> 6] = tw;
     __syncthreads();
     uint32_t tau = s_tau[0];
 #pragma unroll
     for (int w = 1; w < kWaves; ++w) tau = min(tau, s_tau[w]);
-    float tau_f = (tau > kNegInfKey) ? okey_inv(tau) : -INFINITY;
+    return (tau > kNegInfKey) ? okey_inv(tau) : -INFINITY;
+}
+
+// Appends this thread's elements >= tau to its wave's LDS region (keys/vals,
+// capacity wcap) by ballot compaction (no atomics); returns the wave's count,
+// which may exceed wcap (entries past it are dropped).  A lane whose second
+// largest value is below tau holds at most one candidate, its maximum, which
+// the stream already located; only lanes with two or more candidates scan
+// their vectors.
+template <typename T, int NV>
+__device__ __forceinline__ int chunk_extract(const ChunkRegs<T, NV> &cr, int c0, float tau, uint64_t *keys,
+                                             float *vals, int wcap) {
+    constexpr int VEC = VecTraits<T>::VEC;
+    const int tid = threadIdx.x;
+    const bool multi = cr.m2 >= tau;
+    const bool one = !multi && cr.m1 >= tau;
+    int cnt = 0;
+    {
+        const uint64_t m = ballot(one);
+        const int pos = lanes_below(m);
+        if (one && pos < wcap) {
+            keys[pos] = ckey(cr.m1, cr.id1);
+            vals[pos] = cr.m1;
+        }
+        cnt = __popcll(m);
+    }
+    if (ballot(multi)) {
 #pragma unroll
-    for (int j = 0; j < NV; ++j) {
-        int e0 = c0 + (j * kThreads + tid) * VEC;
+        for (int j = 0; j < NV; ++j) {
+            if (ballot(multi && cr.m4[j] >= tau)) {
+                const int id0 = c0 + (j * kThreads + tid) * VEC;
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-            float x = cr.x[j * VEC + e];
-            if (e0 + e < c1 && x >= tau_f) {
-                int pos = atomicAdd(s_nc, 1);
-                if (pos < cap) {
-                    s_key[pos] = ckey(x, (uint32_t)(e0 + e));
-                    s_val[pos] = x;
+                for (int e = 0; e < VEC; ++e) {
+                    const float x = cr.x[j * VEC + e];
+                    const bool p = multi && x >= tau;
+                    const uint64_t m = ballot(p);
+                    if (m) {
+                        const int pos = cnt + lanes_below(m);
+                        if (p && pos < wcap) {
+                            keys[pos] = ckey(x, (uint32_t)(id0 + e));
+                            vals[pos] = x;
+                        }
+                        cnt += __popcll(m);
+                    }
                 }
             }
         }
     }
-    __syncthreads();
-    return *s_nc;
+    return cnt;
 }
 
 // Wave 0 helper: given 256 histogram bins, find digit d (scanning from 255
@@ -285,7 +402,7 @@ __device__ __forceinline__ void find_digit(const uint32_t *bins, int rem, int *o
 // Block radix select over unique 64-bit keys: returns T such that exactly
 // `need` of the keys are >= T.  `src(prefix, shift, bins)` must add, for each
 // key it owns whose bits above shift+8 equal prefix's, one to
-// bins[(key >> shift) & 255].  Requires need >= 1 and at least `need` keys.
+// bins[(key >> shift) & 255].  Requires 1 <= need <= number of keys.
 template <class Src>
 __device__ __forceinline__ uint64_t block_select(Src src, int need, uint32_t *bins, int *s_dig) {
     const int tid = threadIdx.x;
@@ -308,22 +425,25 @@ __device__ __forceinline__ uint64_t block_select(Src src, int need, uint32_t *bi
     }
 }
 
+__device__ __forceinline__ void hist_add(uint64_t k, uint64_t prefix, int shift, uint32_t *bins) {
+    bool match = (shift == 56) || ((k >> (shift + 8)) == (prefix >> (shift + 8)));
+    if (match) atomicAdd(&bins[(k >> shift) & 255u], 1u);
+}
+
 struct LdsKeySrc {
     const uint64_t *keys;
     int n;
     __device__ void operator()(uint64_t prefix, int shift, uint32_t *bins) const {
-        for (int i = threadIdx.x; i < n; i += kThreads) {
-            uint64_t k = keys[i];
-            bool match = (shift == 56) || ((k >> (shift + 8)) == (prefix >> (shift + 8)));
-            if (match) atomicAdd(&bins[(k >> shift) & 255u], 1u);
-        }
+        for (int i = threadIdx.x; i < n; i += kThreads) hist_add(keys[i], prefix, shift, bins);
     }
 };
 
 template <typename T, int NV>
 struct RegKeySrc {
     const ChunkRegs<T, NV> *cr;
-    int c0, c1;
+    int c0;
+    const uint64_t *extra;  // diverted (penalized) entries
+    int n_extra;
     __device__ void operator()(uint64_t prefix, int shift, uint32_t *bins) const {
         constexpr int VEC = VecTraits<T>::VEC;
         const int tid = threadIdx.x;
@@ -333,147 +453,259 @@ struct RegKeySrc {
 #pragma unroll
             for (int e = 0; e < VEC; ++e) {
                 float x = cr->x[j * VEC + e];
-                if (e0 + e < c1 && x == x) {
-                    uint64_t k = ckey(x, (uint32_t)(e0 + e));
-                    bool match = (shift == 56) || ((k >> (shift + 8)) == (prefix >> (shift + 8)));
-                    if (match) atomicAdd(&bins[(k >> shift) & 255u], 1u);
-                }
+                if (x == x) hist_add(ckey(x, (uint32_t)(e0 + e)), prefix, shift, bins);
             }
         }
+        for (int i = tid; i < n_extra; i += kThreads) hist_add(extra[i], prefix, shift, bins);
     }
 };
 
-// Overflow path of stage A: the chunk had more than `cap` candidates.  Select
-// exactly min(k, valid) of them by radix select over the registers and
-// rebuild the LDS list.  Rare (needs many equal or clustered values).
+// Writes the keys (unique) of keys/vals[0..n) ranked by key descending to
+// okeys/ovals[rank] for rank < need.  One key per thread per round; the
+// comparisons read 16 keys per LDS round trip.
+__device__ __forceinline__ void rank_sort(const uint64_t *keys, const float *vals, int n, int need, uint64_t *okeys,
+                                          float *ovals) {
+    for (int i = threadIdx.x; i < n; i += kThreads) {
+        const uint64_t mine = keys[i];
+        int rank = 0;
+        int j = 0;
+        for (; j + 16 <= n; j += 16) {
+            uint64_t b[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) b[u] = keys[j + u];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) rank += (int)(b[u] > mine);
+        }
+        for (; j < n; ++j) rank += (int)(keys[j] > mine);
+        if (rank < need) {
+            okeys[rank] = mine;
+            ovals[rank] = vals[i];
+        }
+    }
+}
+
+// ------------------------------------------------------ stage A, complete
+// Scratch layout per (row, chunk): kCapA keys, kCapA values, one count.
+struct ChunkOut {
+    uint64_t *key;
+    float *val;
+    int32_t *cnt;
+};
+
 template <typename T, int NV>
-__device__ __forceinline__ int chunk_candidates_exact(const ChunkRegs<T, NV> &cr, int c0, int c1, int k,
-                                                      uint64_t *s_key, float *s_val, int *s_nc, uint32_t *bins,
-                                                      int *s_dig) {
-    constexpr int VEC = VecTraits<T>::VEC;
-    const int tid = threadIdx.x;
-    RegKeySrc<T, NV> src{&cr, c0, c1};
-    uint64_t T0 = block_select(src, k, bins, s_dig);
-    if (tid == 0) *s_nc = 0;
+struct SelectLds {
+    uint64_t wkey[kWaves][kWaveCap];  // wave-private candidate regions
+    float wval[kWaves][kWaveCap];
+    uint64_t ckey[kWaves * kWaveCap];  // gathered candidates
+    float cval[kWaves * kWaveCap];
+    uint64_t skey[kCapA];  // sorted top-k
+    float sval[kCapA];
+};
+
+// Stage A after chunk_stream: find the chunk's exact top-min(k, selectable)
+// sorted by (value desc, id asc), publish it to `out` (agent-scope stores).
+// LDS: `sl` (SelectLds), `t`/`fl` when HAS_PEN, small scalars.
+template <typename T, int NV, bool HAS_PEN>
+__device__ __forceinline__ void chunk_select_publish(const RowSource &a, const RowPen &rp, ChunkRegs<T, NV> &cr,
+                                                     float tmax, int c0, int k, SelectLds<T, NV> &sl,
+                                                     PenTable *t, FlagList *fl, uint32_t *s_tau, int *s_wcnt,
+                                                     int *s_n, uint32_t *bins, int *s_dig, ChunkOut out) {
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const float tau = chunk_tau(tmax, k, s_tau);  // contains a barrier (fl->n final after it)
+    int wc = chunk_extract<T, NV>(cr, c0, tau, sl.wkey[wid], sl.wval[wid], kWaveCap);
+    if (lane == 0) s_wcnt[wid] = wc;
+    int nf = 0;
+    if (HAS_PEN) nf = fl->n;
     __syncthreads();
+    int off[kWaves + 1];
+    off[0] = 0;
+    bool overflow = false;
 #pragma unroll
-    for (int j = 0; j < NV; ++j) {
-        int e0 = c0 + (j * kThreads + tid) * VEC;
+    for (int w = 0; w < kWaves; ++w) {
+        overflow |= s_wcnt[w] > kWaveCap;
+        off[w + 1] = off[w] + min(s_wcnt[w], kWaveCap);
+    }
+    int n = off[kWaves];
+    // gather the wave regions contiguously, then the diverted entries >= tau
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-            float x = cr.x[j * VEC + e];
-            if (e0 + e < c1 && x == x) {
-                uint64_t key = ckey(x, (uint32_t)(e0 + e));
-                if (key >= T0) {
-                    int pos = atomicAdd(s_nc, 1);
-                    if (pos < kCapA) {
-                        s_key[pos] = key;
-                        s_val[pos] = x;
+    for (int w = 0; w < kWaves; ++w)
+        for (int i = tid; i < off[w + 1] - off[w]; i += kThreads) {
+            sl.ckey[off[w] + i] = sl.wkey[w][i];
+            sl.cval[off[w] + i] = sl.wval[w][i];
+        }
+    if (HAS_PEN) {
+        if (tid == 0) *s_n = n;
+        __syncthreads();
+        for (int i = tid; i < nf; i += kThreads) {
+            uint32_t id;
+            float v = flag_value(a, *t, *fl, rp, i, id);
+            if (v >= tau) {
+                int pos = atomicAdd(s_n, 1);
+                if (pos < kWaves * kWaveCap) {
+                    sl.ckey[pos] = ckey(v, id);
+                    sl.cval[pos] = v;
+                } else {
+                    overflow = true;
+                }
+            }
+        }
+        __syncthreads();
+        n = *s_n;
+        if (n > kWaves * kWaveCap) overflow = true;
+    }
+    __syncthreads();
+    overflow = __syncthreads_or(overflow);
+    if (overflow) {
+        // More candidates than the buffers hold (clustered or tied values):
+        // exact radix select over registers + diverted entries, then rebuild.
+        uint64_t *extra = sl.skey;  // reuse: penalized keys (<= kFlagMax fits in ckey)
+        int ne = 0;
+        if (HAS_PEN) {
+            for (int i = tid; i < nf; i += kThreads) {
+                uint32_t id;
+                float v = flag_value(a, *t, *fl, rp, i, id);
+                sl.ckey[i] = ckey(v, id);
+                sl.cval[i] = v;
+            }
+            ne = nf;
+            __syncthreads();
+        }
+        (void)extra;
+        RegKeySrc<T, NV> src{&cr, c0, sl.ckey, ne};
+        uint64_t T0 = block_select(src, k, bins, s_dig);
+        if (tid == 0) *s_n = 0;
+        __syncthreads();
+        constexpr int VEC = VecTraits<T>::VEC;
+        // penalized entries first (they sit in ckey[0..ne)); collect into skey
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            int e0 = c0 + (j * kThreads + tid) * VEC;
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) {
+                float x = cr.x[j * VEC + e];
+                if (x == x) {
+                    uint64_t key = ckey(x, (uint32_t)(e0 + e));
+                    if (key >= T0) {
+                        int pos = atomicAdd(s_n, 1);
+                        if (pos < kCapA) {
+                            sl.skey[pos] = key;
+                            sl.sval[pos] = x;
+                        }
                     }
                 }
             }
         }
-    }
-    __syncthreads();
-    return min(*s_nc, kCapA);
-}
-
-// Publishes the chunk's candidates, then takes a ticket; returns true in the
-// last workgroup of the row (which then owns the row's merge).  The last
-// workgroup re-arms the ticket for the next launch.
-__device__ __forceinline__ bool publish_and_ticket(const uint64_t *s_key, const float *s_val, int nc,
-                                                   uint64_t *g_key, float *g_val, int32_t *g_cnt, int32_t *tickets,
-                                                   int row, int g, int G, int *s_flag) {
-    const int tid = threadIdx.x;
-    uint64_t *dk = g_key + ((int64_t)row * G + g) * kCapA;
-    float *dv = g_val + ((int64_t)row * G + g) * kCapA;
-    for (int i = tid; i < nc; i += kThreads) {
-        dk[i] = s_key[i];
-        dv[i] = s_val[i];
-    }
-    if (tid == 0) g_cnt[row * G + g] = nc;
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) *s_flag = (atomicAdd(&tickets[row], 1) == G - 1);
-    __syncthreads();
-    bool last = *s_flag != 0;
-    if (last) {
-        __threadfence();
-        if (tid == 0) tickets[row] = 0;
-    }
-    return last;
-}
-
-// Stage B gather: loads all published candidates of `row` into LDS and returns
-// their number (<= G * kCapA).
-__device__ __forceinline__ int gather_candidates(const uint64_t *g_key, const float *g_val, const int32_t *g_cnt,
-                                                 int row, int G, uint64_t *b_key, float *b_val, int *s_off) {
-    const int tid = threadIdx.x;
-    if (tid == 0) {
-        int o = 0;
-        for (int g = 0; g < G; ++g) {
-            s_off[g] = o;
-            o += __hip_atomic_load(&g_cnt[row * G + g], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        s_off[G] = o;
-    }
-    __syncthreads();
-    for (int g = 0; g < G; ++g) {
-        int o = s_off[g], n = s_off[g + 1] - o;
-        const uint64_t *sk = g_key + ((int64_t)row * G + g) * kCapA;
-        const float *sv = g_val + ((int64_t)row * G + g) * kCapA;
-        for (int i = tid; i < n; i += kThreads) {
-            b_key[o + i] = sk[i];
-            b_val[o + i] = sv[i];
-        }
-    }
-    int N = s_off[G];
-    __syncthreads();
-    return N;
-}
-
-// Stage B: reduce N unique candidates to the top `need` sorted by key desc
-// into o_key/o_val[0..need).  need <= 256 and need <= N.
-__device__ __forceinline__ void select_sorted(const uint64_t *b_key, const float *b_val, int N, int need,
-                                              uint64_t *o_key, float *o_val, uint64_t *t_key, float *t_val,
-                                              uint32_t *bins, int *s_dig, int *s_cnt) {
-    const int tid = threadIdx.x;
-    const uint64_t *ck = b_key;
-    const float *cv = b_val;
-    if (N > need) {
-        LdsKeySrc src{b_key, N};
-        uint64_t T0 = block_select(src, need, bins, s_dig);
-        if (tid == 0) *s_cnt = 0;
-        __syncthreads();
-        for (int i = tid; i < N; i += kThreads) {
-            uint64_t k = b_key[i];
-            if (k >= T0) {
-                int pos = atomicAdd(s_cnt, 1);
-                if (pos < kThreads) {
-                    t_key[pos] = k;
-                    t_val[pos] = b_val[i];
+        for (int i = tid; i < ne; i += kThreads) {
+            if (sl.ckey[i] >= T0) {
+                int pos = atomicAdd(s_n, 1);
+                if (pos < kCapA) {
+                    sl.skey[pos] = sl.ckey[i];
+                    sl.sval[pos] = sl.cval[i];
                 }
             }
         }
         __syncthreads();
-        ck = t_key;
-        cv = t_val;
+        n = min(*s_n, kCapA);
+        __syncthreads();
+        for (int i = tid; i < n; i += kThreads) {
+            sl.ckey[i] = sl.skey[i];
+            sl.cval[i] = sl.sval[i];
+        }
+        __syncthreads();
     }
-    // rank sort: rank = number of keys greater (keys are unique)
-    uint64_t mine = 0;
-    float mv = 0.0f;
-    int rank = 0;
-    if (tid < need) {
-        mine = ck[tid];
-        mv = cv[tid];
-        for (int j = 0; j < need; ++j) rank += (ck[j] > mine) ? 1 : 0;
+    const int m = min(n, k);
+    rank_sort(sl.ckey, sl.cval, n, m, sl.skey, sl.sval);
+    __syncthreads();
+    for (int i = tid; i < m; i += kThreads) {
+        st_agent(&out.key[i], sl.skey[i]);
+        st_agent(&out.val[i], sl.sval[i]);
+    }
+    if (tid == 0) st_agent(out.cnt, m);
+}
+
+// ------------------------------------------------------------- stage B
+// Loads the G sorted chunk lists of a row (one round trip: every slot is
+// requested before any is used) and merges them: the rank of an entry is its
+// index in its own list plus, for every other list, the number of entries
+// greater than it (binary search, all lists in parallel).  Writes the row's
+// top-min(k, total) to okey/oval sorted; returns that count.
+struct MergeLds {
+    uint64_t key[kMaxG][kCapA];
+    float val[kMaxG][kCapA];
+    int cnt[kMaxG];
+};
+
+__device__ __forceinline__ int row_merge(const uint64_t *g_key, const float *g_val, const int32_t *g_cnt, int row,
+                                         int G, int k, MergeLds &ml, uint64_t *okey, float *oval) {
+    const int tid = threadIdx.x;
+    constexpr int kPer = (kMaxG * kCapA) / kThreads;  // slots per thread (max)
+    uint64_t kk[kPer];
+    float vv[kPer];
+    const int slots = G * k;
+    const int64_t rb = (int64_t)row * G;
+    int cn = 0;
+    if (tid < G) cn = ld_agent(&g_cnt[rb + tid]);
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        int s = tid + u * kThreads;
+        if (s < slots) {
+            int g = s / k, i = s - g * k;
+            kk[u] = ld_agent(&g_key[(rb + g) * kCapA + i]);
+            vv[u] = ld_agent(&g_val[(rb + g) * kCapA + i]);
+        }
+    }
+    if (tid < G) ml.cnt[tid] = cn;
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        int s = tid + u * kThreads;
+        if (s < slots) {
+            int g = s / k, i = s - g * k;
+            ml.key[g][i] = kk[u];
+            ml.val[g][i] = vv[u];
+        }
     }
     __syncthreads();
-    if (tid < need) {
-        o_key[rank] = mine;
-        o_val[rank] = mv;
+    int total = 0;
+    for (int g = 0; g < G; ++g) total += ml.cnt[g];
+    const int need = min(k, total);
+    int half = 1;
+    while (half * 2 <= k) half *= 2;  // largest power of two <= k
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        int s = tid + u * kThreads;
+        if (s >= slots) continue;
+        int g = s / k, i = s - g * k;
+        if (i >= ml.cnt[g]) continue;
+        const uint64_t mine = ml.key[g][i];
+        // pos[h] = number of entries of list h greater than mine, found by a
+        // branch-free power-of-two search advanced for all lists in lock-step
+        int pos[kMaxG];
+        int len[kMaxG];
+#pragma unroll
+        for (int h = 0; h < kMaxG; ++h) {
+            pos[h] = 0;
+            len[h] = (h < G && h != g) ? ml.cnt[h] : 0;
+        }
+        for (int st = half; st > 0; st >>= 1) {
+#pragma unroll
+            for (int h = 0; h < kMaxG; ++h) {
+                if (h < G) {
+                    const int probe = pos[h] + st;
+                    const uint64_t kv = ml.key[h][min(probe, kCapA) - 1];
+                    pos[h] += (probe <= len[h] && kv > mine) ? st : 0;
+                }
+            }
+        }
+        int rank = i;
+#pragma unroll
+        for (int h = 0; h < kMaxG; ++h) rank += pos[h];
+        if (rank < need) {
+            okey[rank] = mine;
+            oval[rank] = ml.val[g][i];
+        }
     }
     __syncthreads();
+    return need;
 }
 
 }  // namespace zi

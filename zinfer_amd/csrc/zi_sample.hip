@@ -3,33 +3,36 @@
 //
 // One launch covers the batch: grid = rows x G workgroups.  Stage A (every
 // workgroup) streams its chunk of the row from HBM once with 16-byte loads,
-// applies mask + penalties + edits in registers and publishes a superset of
-// the chunk's top-k.  The last workgroup of each row (ticket counter) runs
-// stage B: gathers the row's candidates, radix-selects the exact top-k by
-// (value desc, id asc), sorts them and runs the reference tail on one wave:
-// untempered top-p and min-p, temperature weights, XTC and the draw, with
-// every sum in the reference's sequential f32 order.
+// applies mask + penalties + edits, and publishes the chunk's exact top-k
+// sorted by (value desc, id asc).  The last workgroup of each row (ticket
+// counter) runs stage B: merges the G sorted lists into the row's top-k and
+// runs the reference tail on one wave: untempered top-p and min-p,
+// temperature weights, XTC and the draw, with every sum in the reference's
+// sequential f32 order.
 #include "zi_launch.hpp"
 #include "zi_rowpass.hpp"
 
 namespace zi {
 
-struct SmemSampleA {
+template <bool P>
+struct PenLds {
     PenTable pen;
-    uint64_t ckey[kCapA];
-    float cval[kCapA];
+    FlagList fl;
 };
-struct SmemSampleB {
-    uint64_t bkey[kMaxG * kCapA];
-    float bval[kMaxG * kCapA];
-    uint64_t tkey[kThreads];
-    float tval[kThreads];
+template <>
+struct PenLds<false> {
+    PenTable *pen_ptr() { return nullptr; }
+};
+
+template <typename T, int NV, bool HAS_PEN>
+struct SampleStageA {
+    PenLds<HAS_PEN> p;
+    SelectLds<T, NV> sel;
+};
+struct SampleStageB {
+    MergeLds ml;
     uint64_t okey[kThreads];
     float oval[kThreads];
-};
-union SmemSample {
-    SmemSampleA a;
-    SmemSampleB b;
 };
 
 // Sequential f32 sum of x_i over lanes/chunks for i in [0, end) (x must be 0
@@ -47,82 +50,54 @@ __device__ __forceinline__ float chain_sum(const float (&x)[4], int end) {
     return carry;
 }
 
-template <typename T, int NV>
-__global__ __launch_bounds__(kThreads) void sample_kernel(SampleParams P) {
-    __shared__ SmemSample sm;
-    __shared__ uint32_t s_bins[256];
-    __shared__ uint32_t s_tau[kWaves];
-    __shared__ int s_dig[2];
-    __shared__ int s_nc, s_flag, s_cnt;
-    __shared__ int s_off[kMaxG + 1];
-
-    const RowSource &a = P.src;
-    const int tid = threadIdx.x;
-    const int G = a.G;
-    const int row = blockIdx.x / G;
-    const int g = blockIdx.x - row * G;
-    const int c0 = g * a.CH;
-    const int c1 = min(a.V, c0 + a.CH);
-
-    RowPen rp = row_pen(a, row);
-    PenRegs pr;
-    if (rp.any) pen_fetch(rp, pr);
-    uint4 raw[NV];
-    uint32_t mw[NV];
-    chunk_load<T, NV>(a, row, c0, c1, raw, mw);
-    if (rp.any) pen_build(sm.a.pen, rp, pr, c0, c1);
-    ChunkRegs<T, NV> cr;
-    float tmax = chunk_transform<T, NV>(a, sm.a.pen, rp, c0, c1, raw, mw, cr);
-
-    const int k = P.k;
-    int nc = chunk_candidates<T, NV>(cr, tmax, c0, c1, k, sm.a.ckey, sm.a.cval, kCapA, &s_nc, s_tau);
-    if (nc > kCapA) nc = chunk_candidates_exact<T, NV>(cr, c0, c1, k, sm.a.ckey, sm.a.cval, &s_nc, s_bins, s_dig);
-    if (!publish_and_ticket(sm.a.ckey, sm.a.cval, nc, P.g_key, P.g_val, P.g_cnt, P.tickets, row, g, G, &s_flag))
-        return;
-
-    // ---------------- stage B: the last workgroup of this row ----------------
-    int N = gather_candidates(P.g_key, P.g_val, P.g_cnt, row, G, sm.b.bkey, sm.b.bval, s_off);
-    const int n = min(k, N);
-    if (n == 0) {  // no selectable logit (every entry NaN): outside the reference contract
-        if (tid == 0) {
-            P.tok[row] = 0u;
-            P.margin[row] = 10.0f;
-            if (P.ndraws) P.ndraws[row] = 0;
-            if (P.keep) P.keep[row] = 0;
-        }
-        return;
-    }
-    select_sorted(sm.b.bkey, sm.b.bval, N, n, sm.b.okey, sm.b.oval, sm.b.tkey, sm.b.tval, s_bins, s_dig, &s_cnt);
-    if (tid >= 64) return;  // the tail runs on wave 0 with all 64 lanes active
-
-    const int lane = tid;
+// The reference tail (src/sampler.zig:211-275) on the row's n sorted
+// candidates, one wave with all 64 lanes active.
+__device__ __forceinline__ void sample_tail(const SampleParams &P, int row, const uint64_t *okey, const float *oval,
+                                            int n) {
+    const int lane = threadIdx.x;
     float cv[4];
     uint32_t cid[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
         int i = lane + 64 * c;
-        cv[c] = (i < n) ? sm.b.oval[i] : 0.0f;
-        cid[c] = (i < n) ? ckey_id(sm.b.okey[i]) : 0u;
+        cv[c] = (i < n) ? oval[i] : 0.0f;
+        cid[c] = (i < n) ? ckey_id(okey[i]) : 0u;
     }
-    const float mx = sm.b.oval[0];  // sampler.zig:212-213
-    const float margin = (n >= 2) ? mx - sm.b.oval[1] : 10.0f;
+    const float mx = oval[0];  // :212-213
+    const float margin = (n >= 2) ? mx - oval[1] : 10.0f;
     int keep = n;
 
-    // top-p then min-p on untempered exp(v - mx) (sampler.zig:215-234)
-    float e[4];
+    // top-p then min-p on untempered exp(v - mx) (:215-234).  The
+    // temperature weights are computed alongside (used for i < keep only).
+    const float inv_t = 1.0f / P.temp;
+    float e[4], w[4];
     const bool use_e = (P.top_p < 1.0f) || (P.min_p > 0.0f);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) e[c] = (use_e && lane + 64 * c < n) ? exp32(cv[c] - mx) : 0.0f;
+    for (int c = 0; c < 4; ++c) {
+        const bool in = lane + 64 * c < n;
+        e[c] = (use_e && in) ? exp32(cv[c] - mx) : 0.0f;
+        w[c] = in ? exp32((cv[c] - mx) * inv_t) : 0.0f;
+    }
     if (P.top_p < 1.0f) {
+        // Every prefix sum is >= e_0 = 1, whose half ulp is 2^-24: a term below
+        // that cannot change the sum, and the terms are non-increasing, so the
+        // sequential sum ends at the first such term (exactly).
+        // (NaN terms, from an infinite maximum, stay live: the reference's sums
+        // are then NaN and nothing is cut.)
+        const int live = __popcll(ballot(lane < n && !(e[0] < 0x1p-24f))) +
+                         __popcll(ballot(lane + 64 < n && !(e[1] < 0x1p-24f))) +
+                         __popcll(ballot(lane + 128 < n && !(e[2] < 0x1p-24f))) +
+                         __popcll(ballot(lane + 192 < n && !(e[3] < 0x1p-24f)));
         float pc[4];
         float carry = 0.0f;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            pc[c] = 0.0f;
-            if (64 * c < n) {
-                int steps = min(64, n - 64 * c);
-                pc[c] = wave_serial_chain<false>(e[c], carry, steps);
-                carry = readlane_f(pc[c], steps - 1);
+            pc[c] = carry;
+            if (64 * c < live) {
+                int steps = min(64, live - 64 * c);
+                float p = wave_serial_chain<false>(e[c], carry, steps);
+                pc[c] = (lane < steps) ? p : readlane_f(p, steps - 1);
+                carry = readlane_f(p, steps - 1);
             }
         }
         const float thr = P.top_p * carry;  // carry == total
@@ -147,14 +122,12 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleParams P) {
         }
     }
 
-    // temperature on the survivors (sampler.zig:236-242)
-    const float inv_t = 1.0f / P.temp;
-    float w[4];
+    // temperature on the survivors (:236-242)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) w[c] = (lane + 64 * c < keep) ? exp32((cv[c] - mx) * inv_t) : 0.0f;
+    for (int c = 0; c < 4; ++c) w[c] = (lane + 64 * c < keep) ? w[c] : 0.0f;
     float total = chain_sum(w, keep);
 
-    // XTC (sampler.zig:244-268)
+    // XTC (:244-268)
     int start = 0;
     int draws = 0;
     const float u0 = P.uniforms[2 * row];
@@ -187,13 +160,8 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleParams P) {
     }
     draws += 1;
 
-    // draw: r = u * total; r -= w_i until r <= 0 (sampler.zig:270-275)
-    uint32_t last_col = cid[0];
-    const int lq = (keep - 1) >> 6;
-    if (lq == 1) last_col = cid[1];
-    if (lq == 2) last_col = cid[2];
-    if (lq == 3) last_col = cid[3];
-    uint32_t tok = __builtin_amdgcn_readlane(last_col, (keep - 1) & 63);  // fallback c[keep-1] (:275)
+    // draw: r = u * total; r -= w_i until r <= 0 (:270-275)
+    uint32_t tok = ckey_id(okey[keep - 1]);  // fallback c[keep-1] (:275)
     {
         float carry = umain * total;
 #pragma unroll
@@ -205,8 +173,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleParams P) {
                 float d = wave_serial_chain<true>(x, carry, steps);
                 uint64_t m = ballot(i >= start && i < keep && d <= 0.0f);
                 if (m) {
-                    int l = __ffsll((unsigned long long)m) - 1;
-                    tok = __builtin_amdgcn_readlane(cid[c], l);
+                    tok = ckey_id(okey[64 * c + __ffsll((unsigned long long)m) - 1]);
                     break;
                 }
                 carry = readlane_f(d, steps - 1);
@@ -234,25 +201,86 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleParams P) {
     }
 }
 
-template <typename T, int NV>
+template <typename T, int NV, bool HAS_MASK, bool HAS_PEN>
+__global__ __launch_bounds__(kThreads) void sample_kernel(SampleParams P) {
+    __shared__ union {
+        SampleStageA<T, NV, HAS_PEN> a;
+        SampleStageB b;
+    } sm;
+    __shared__ uint32_t s_bins[256];
+    __shared__ uint32_t s_tau[kWaves];
+    __shared__ int s_wcnt[kWaves];
+    __shared__ int s_dig[2];
+    __shared__ int s_n, s_flag;
+
+    const RowSource &a = P.src;
+    const int tid = threadIdx.x;
+    const int G = a.G;
+    const int row = blockIdx.x / G;
+    const int g = blockIdx.x - row * G;
+    const int c0 = g * a.CH;
+    const int c1 = min(a.V, c0 + a.CH);
+    const int k = P.k;
+
+    RowPen rp = row_pen(a, row);
+    PenTable *pen = nullptr;
+    FlagList *fl = nullptr;
+    if constexpr (HAS_PEN) {
+        pen = &sm.a.p.pen;
+        fl = &sm.a.p.fl;
+    }
+    ChunkRegs<T, NV> cr;
+    float tmax = chunk_stream<T, NV, HAS_MASK, HAS_PEN>(a, row, c0, c1, cr, pen, fl, rp);
+    const int64_t rg = (int64_t)row * G + g;
+    ChunkOut out{P.g_key + rg * kCapA, P.g_val + rg * kCapA, P.g_cnt + rg};
+    chunk_select_publish<T, NV, HAS_PEN>(a, rp, cr, tmax, c0, k, sm.a.sel, pen, fl, s_tau, s_wcnt, &s_n, s_bins,
+                                         s_dig, out);
+    if (!row_ticket(P.tickets, row, G, &s_flag)) return;
+
+    // ---------------- stage B: the last workgroup of this row ----------------
+    const int n = row_merge(P.g_key, P.g_val, P.g_cnt, row, G, k, sm.b.ml, sm.b.okey, sm.b.oval);
+    if (tid >= 64) return;  // the tail runs on wave 0 with all 64 lanes active
+    if (n == 0) {           // no selectable logit (every entry NaN): outside the reference contract
+        if (tid == 0) {
+            P.tok[row] = 0u;
+            P.margin[row] = 10.0f;
+            if (P.ndraws) P.ndraws[row] = 0;
+            if (P.keep) P.keep[row] = 0;
+        }
+        return;
+    }
+    sample_tail(P, row, sm.b.okey, sm.b.oval, n);
+}
+
+template <typename T, int NV, bool M, bool PN>
 static hipError_t launch_sample_t(const SampleParams &P, int rows, hipStream_t st) {
     dim3 grid(rows * P.src.G), block(kThreads);
-    hipLaunchKernelGGL((sample_kernel<T, NV>), grid, block, 0, st, P);
+    hipLaunchKernelGGL((sample_kernel<T, NV, M, PN>), grid, block, 0, st, P);
     return hipGetLastError();
+}
+
+template <typename T, int NV>
+static hipError_t launch_sample_nv(const SampleParams &P, int rows, hipStream_t st) {
+    const bool m = P.src.mask != nullptr;
+    const bool p = (P.src.hist != nullptr) || (P.src.edit_ids != nullptr);
+    if (m && p) return launch_sample_t<T, NV, true, true>(P, rows, st);
+    if (m) return launch_sample_t<T, NV, true, false>(P, rows, st);
+    if (p) return launch_sample_t<T, NV, false, true>(P, rows, st);
+    return launch_sample_t<T, NV, false, false>(P, rows, st);
 }
 
 hipError_t launch_sample(const SampleParams &P, int dtype, int nv, int rows, hipStream_t st) {
     if (dtype == 0) {
         switch (nv) {
-            case 4: return launch_sample_t<float, 4>(P, rows, st);
-            case 8: return launch_sample_t<float, 8>(P, rows, st);
-            default: return launch_sample_t<float, 16>(P, rows, st);
+            case 4: return launch_sample_nv<float, 4>(P, rows, st);
+            case 8: return launch_sample_nv<float, 8>(P, rows, st);
+            default: return launch_sample_nv<float, 16>(P, rows, st);
         }
     }
     switch (nv) {
-        case 2: return launch_sample_t<uint16_t, 2>(P, rows, st);
-        case 4: return launch_sample_t<uint16_t, 4>(P, rows, st);
-        default: return launch_sample_t<uint16_t, 8>(P, rows, st);
+        case 2: return launch_sample_nv<uint16_t, 2>(P, rows, st);
+        case 4: return launch_sample_nv<uint16_t, 4>(P, rows, st);
+        default: return launch_sample_nv<uint16_t, 8>(P, rows, st);
     }
 }
 
