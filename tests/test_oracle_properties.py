@@ -1,0 +1,266 @@
+"""Pins for the oracle beyond the reference's KATs: hand-derived values and
+independent formulations (numpy / scipy / brute force), each chosen so that a
+plausible restatement mistake -- a wrong tie rule, a tempered top-p, an f64
+or reassociated sum, `<` for `<=`, a dropped term -- fails."""
+import numpy as np
+import pytest
+
+
+def exp32(x):
+    return np.float32(np.exp(np.float64(np.float32(x))))
+
+
+# ------------------------------------------------------------------ top-k
+@pytest.mark.parametrize("seed", range(6))
+@pytest.mark.parametrize("k", [1, 7, 40, 0])
+def test_topk_order_is_value_desc_id_asc(oracle, seed, k):
+    """Insertion top-k (k < V, sampler.zig:203-209) and stable sort (k = V,
+    :198-201) both yield the first k of lexsort(id asc, value desc), with
+    -0.0 tying +0.0."""
+    rng = np.random.default_rng(seed)
+    V = 300
+    x = rng.integers(-3, 4, V).astype(np.float32)  # heavy ties
+    x[x == 0] = np.where(rng.random((x == 0).sum()) < 0.5, -0.0, 0.0)
+    p = oracle.params(temp=1.0, top_k=k, top_p=1.0, min_p=0.0)
+    kk = V if k == 0 else k
+    _, _, diag = oracle.sample_row(p, x, [0.5, 0.5], cap=kk)
+    order = np.lexsort((np.arange(V), -x.astype(np.float64)))[:kk]
+    assert np.array_equal(diag["ids"], order.astype(np.uint32))
+
+
+# ------------------------------------------------------------------ top-p
+def _sorted_candidates(x, k):
+    order = np.lexsort((np.arange(x.size), -x.astype(np.float64)))[:k]
+    return x[order], order
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_top_p_keep_is_sequential_f32_over_untempered_weights(oracle, seed):
+    """keep = first i with acc_i >= top_p * total, acc and total sequential f32
+    sums of exp(v - max) over the top-k (sampler.zig:215-228), independent of
+    temperature.  numpy's float32 add.accumulate is a sequential sum."""
+    rng = np.random.default_rng(100 + seed)
+    x = (rng.standard_normal(2000) * 2).astype(np.float32)
+    k, top_p = 64, np.float32(rng.uniform(0.3, 0.99))
+    v, _ = _sorted_candidates(x, k)
+    e = np.array([exp32(vi - v[0]) for vi in v], np.float32)
+    acc = np.add.accumulate(e, dtype=np.float32)
+    keep = int(np.argmax(acc >= np.float32(top_p) * acc[-1])) + 1
+    for temp in (0.3, 1.0, 2.5):  # a tempered top-p would move keep
+        p = oracle.params(temp=temp, top_k=k, top_p=float(top_p), min_p=0.0)
+        _, _, diag = oracle.sample_row(p, x, [0.5, 0.5], cap=k)
+        assert diag["keep"] == keep
+
+
+def test_top_p_uses_f32_sequential_total_not_f64():
+    """Terms of exactly half an ulp vanish in a sequential f32 sum (ties to
+    even) but not in f64: 1 + 1000 * 2^-24 stays 1.0f."""
+    e = np.array([1.0] + [2.0 ** -24] * 1000, np.float32)
+    assert np.add.accumulate(e, dtype=np.float32)[-1] == np.float32(1.0)
+    assert float(np.sum(e.astype(np.float64))) > 1.00005
+
+
+def test_top_p_f32_total_decides_keep(oracle):
+    """Logits whose untempered weights are 1 and many tiny equal terms: the
+    sequential f32 total stays 1.0 so top_p = 0.9999 keeps only token 0; an
+    f64 total would keep more."""
+    tiny = np.float32(np.log(2.0 ** -24 * 1.0000001))  # exp32(tiny) rounds to about 2^-24
+    x = np.full(300, tiny, np.float32)
+    x[0] = 0.0
+    p = oracle.params(temp=1.0, top_k=300, top_p=0.9999, min_p=0.0)
+    _, _, diag = oracle.sample_row(p, x, [0.5, 0.5], cap=300)
+    e = exp32(tiny)
+    assert e < 2.0 ** -23  # below one ulp of 1.0: lost in f32, kept in f64
+    assert diag["keep"] == 1
+
+
+# ------------------------------------------------------------------ min-p
+def test_min_p_cut_is_strictly_below(oracle):
+    """min-p keeps candidates with exp(v - max) >= min_p (the cut uses `<`,
+    sampler.zig:230) and never keeps fewer than one (:231)."""
+    x = np.array([10.0, 9.0, 6.0, 1.0] + [-50.0] * 6, np.float32)
+    e1 = float(exp32(np.float32(9.0) - np.float32(10.0)))
+    for min_p, keep in [(0.10, 2), (e1, 2), (np.nextafter(np.float32(e1), np.float32(1)), 1), (1.5, 1)]:
+        p = oracle.params(temp=1.0, top_k=10, top_p=1.0, min_p=float(min_p))
+        _, _, diag = oracle.sample_row(p, x, [0.5, 0.5], cap=10)
+        assert diag["keep"] == keep, (min_p, diag["keep"])
+
+
+# ------------------------------------------------------------------- draw
+def test_draw_boundary_uses_le(oracle):
+    """r = u * total; r -= w_i; the first r <= 0 wins (sampler.zig:270-274).
+    Weights 1, 0.5, 0.5 (exact, total 2): u = 0.5 lands exactly on the first
+    boundary and must pick candidate 0, u just above picks candidate 1."""
+    ln = np.float32(np.log(0.5))
+    x = np.array([0.0, ln, ln] + [-80.0] * 5, np.float32)
+    p = oracle.params(temp=1.0, top_k=8, top_p=1.0, min_p=0.0)
+    _, _, diag = oracle.sample_row(p, x, [0.5, 0.5], cap=8)
+    w = np.array([exp32(v) for v in x[:3]], np.float32)
+    assert w[0] == 1.0 and w[1] == np.float32(0.5) and diag["total"] == 2.0
+    tot = diag["total"]
+    u0 = w[0] / tot  # r = u0 * total == w_0 exactly
+    assert oracle.sample_row(p, x, [u0, 0.5])[0] == 0
+    assert oracle.sample_row(p, x, [np.nextafter(u0, np.float32(1)), 0.5])[0] == 1
+
+
+@pytest.mark.parametrize("temp", [0.6, 1.0, 1.7])
+def test_draw_frequencies_follow_tempered_weights(oracle, temp):
+    """Sweeping u over a fine grid, each kept candidate is drawn with
+    frequency w_i / total where w_i = exp((v_i - max) / T) (sampler.zig:236-242)."""
+    rng = np.random.default_rng(int(temp * 10))
+    x = (rng.standard_normal(500)).astype(np.float32)
+    p = oracle.params(temp=temp, top_k=12, top_p=1.0, min_p=0.0)
+    v, ids = _sorted_candidates(x, 12)
+    w = np.exp((v.astype(np.float64) - v[0]) / temp)
+    w /= w.sum()
+    N = 20000
+    counts = {}
+    for u in (np.arange(N, dtype=np.float64) + 0.5) / N:
+        t = oracle.sample_row(p, x, [np.float32(u), 0.5])[0]
+        counts[t] = counts.get(t, 0) + 1
+    for i, tid in enumerate(ids):
+        assert abs(counts.get(int(tid), 0) / N - w[i]) < 2e-3
+
+
+# ------------------------------------------------------------------- XTC
+def test_xtc_removes_leading_run_above_threshold(oracle):
+    """XTC drops c[0 .. pos_last) where pos_last is the last index of the
+    leading run with p >= threshold (sampler.zig:251-266).  Probabilities
+    0.4, 0.3, 0.2, 0.1 with threshold 0.25: the run is {0, 1}, pos_last = 1,
+    so candidate 0 is removed and 1, 2, 3 remain."""
+    x = np.log(np.array([0.4, 0.3, 0.2, 0.1] + [1e-30] * 4)).astype(np.float32)
+    p = oracle.params(temp=1.0, top_k=8, top_p=1.0, min_p=0.0, xtc_probability=1.0, xtc_threshold=0.25,
+                      xtc_min_keep=1)
+    toks = set()
+    for u in np.linspace(0, 1, 400, endpoint=False):
+        t, _, diag = oracle.sample_row(p, x, [0.0, u], cap=8)
+        assert diag["start"] == 1
+        toks.add(t)
+    assert toks == {1, 2, 3}
+    # chance above the probability: no exclusion, two draws consumed
+    p2 = oracle.params(temp=1.0, top_k=8, top_p=1.0, min_p=0.0, xtc_probability=0.5, xtc_threshold=0.25)
+    _, _, diag = oracle.sample_row(p2, x, [0.75, 0.1], cap=8)
+    assert diag["start"] == 0 and diag["ndraws"] == 2
+
+
+# -------------------------------------------------------------- penalties
+def test_repetition_penalty_hand_values(oracle):
+    """sampler.zig:91-100: positive logits are divided, non-positive
+    multiplied, each distinct id once."""
+    x = np.array([3.0, -2.0, 0.0, 6.0, 1.5], np.float32)
+    out = oracle.apply_penalty(x, [0, 1, 2, 0, 0, 1], 1.5)
+    assert out.tolist() == [2.0, -3.0, 0.0, 6.0, 1.5]
+
+
+def test_frequency_presence_hand_values(oracle):
+    """Extension: l -= count * freq + presence for ids in the window, after
+    the repetition step.  id 0 appears 3 times: 3 - (3*0.5 + 0.25) = 1.25;
+    id 3 once: 6 - (0.5 + 0.25) = 5.25; with rp 2: id 0 -> 1.5 - 1.75."""
+    x = np.array([3.0, 7.0, 1.0, 6.0], np.float32)
+    out = oracle.apply_penalty(x, [0, 3, 0, 0], 1.0, 0.5, 0.25)
+    assert out.tolist() == [1.25, 7.0, 1.0, 5.25]
+    out = oracle.apply_penalty(x, [0, 3, 0, 0], 2.0, 0.5, 0.25)
+    assert out.tolist() == [1.5 - 1.75, 7.0, 1.0, 3.0 - 0.75]
+
+
+def test_dry_matches_brute_force(oracle):
+    """DRY edits (sampler.zig:104-187) against an O(L^2) restatement: for each
+    earlier position, the longest common suffix with the current context
+    (bounded by the breaker limit) names the continuation token."""
+    rng = np.random.default_rng(9)
+    for trial in range(60):
+        L = int(rng.integers(3, 60))
+        hist = rng.integers(0, 5, L).tolist()
+        brk = [4] if trial % 3 == 0 else []
+        allowed = int(rng.integers(1, 4))
+        ids, d = oracle.dry_edits(hist, brk, 0.8, 1.75, allowed, 1024)
+        R = hist[::-1]
+        rep_limit = next((i for i, t in enumerate(R) if t in brk), L)
+        expect = {}
+        if L > allowed and rep_limit >= allowed:
+            for kpos in range(1, L):
+                n = 0
+                while n < min(L - kpos, rep_limit) and R[n] == R[kpos + n]:
+                    n += 1
+                if n >= allowed and R[kpos - 1] not in brk:
+                    expect[R[kpos - 1]] = max(expect.get(R[kpos - 1], 0), n)
+        got = dict(zip(ids.tolist(), d.tolist()))
+        assert set(got) == set(expect), (hist, brk, allowed)
+        for t, n in expect.items():
+            assert abs(got[t] - 0.8 * 1.75 ** (n - allowed)) < 1e-5 * got[t]
+
+
+# ----------------------------------------------------------------- argmax
+def _lane16_model(x):
+    """Independent numpy model of the 2x8-lane SIMD argmax."""
+    V = x.size
+    body = (V // 16) * 16
+    cls = x[:body].reshape(-1, 16)
+    first = np.argmax(cls, axis=0)  # first maximum per class
+    cmax = cls[first, np.arange(16)]
+    cidx = first * 16 + np.arange(16)
+    seq = [(cmax[c], cidx[c]) for j in range(8) for c in (j, j + 8)] + [(x[i], i) for i in range(body, V)]
+    best, second, bi = -np.inf, -np.inf, 0
+    for v, i in seq:
+        if v > best:
+            second, best, bi = best, v, i
+        elif v > second:
+            second = v
+    return int(bi), float(best - second) if second > -np.inf else 10.0
+
+
+def test_argmax_lane16_hand_cases(oracle):
+    x = np.zeros(32, np.float32)
+    x[3] = x[8] = 5.0  # equal maxima: class 8 is reduced before class 3
+    assert oracle.argmax_with_margin(x) == (8, 0.0)
+    y = np.zeros(32, np.float32)
+    y[3], y[19] = 5.0, 4.0  # both in class 3: the 4 is hidden from the margin
+    assert oracle.argmax_with_margin(y) == (3, 5.0)
+    assert oracle.argmax_true(y) == (3, 1.0)
+    z = np.full(20, -np.inf, np.float32)
+    assert oracle.argmax_with_margin(z) == (0, 10.0)
+
+
+@pytest.mark.parametrize("V", [16, 17, 33, 100, 1000, 4097])
+def test_argmax_lane16_model(oracle, V):
+    rng = np.random.default_rng(V)
+    for _ in range(20):
+        x = rng.integers(-2, 3, V).astype(np.float32)
+        assert oracle.argmax_with_margin(x) == _lane16_model(x)
+
+
+def test_argmax_small_v_path(oracle):
+    """V < 16 (sampler.zig:535-551): exact first max; margin x[best] - x[second]."""
+    assert oracle.argmax_with_margin(np.array([1, 3, 3, 2], np.float32)) == (1, 0.0)
+    assert oracle.argmax_with_margin(np.array([5], np.float32)) == (0, 10.0)
+    assert oracle.argmax_with_margin(np.array([2, 7, 1], np.float32)) == (1, 5.0)
+
+
+# ----------------------------------------------------------------- entropy
+@pytest.mark.parametrize("seed", range(4))
+def test_entropy_topk_vs_scipy(oracle, seed):
+    from scipy.special import softmax
+    from scipy.stats import entropy
+
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal(5000) * 2).astype(np.float32)
+    if seed == 1:
+        x[7] += 15.0
+    if seed == 2:
+        x[rng.random(5000) < 0.5] = -np.inf
+    H, ids, probs = oracle.entropy_topk(x, 8)
+    p = softmax(x.astype(np.float64))
+    assert abs(H - entropy(p)) <= 1e-9 * max(1.0, entropy(p))
+    order = np.lexsort((np.arange(x.size), -x.astype(np.float64)))[:8]
+    assert np.array_equal(ids, order.astype(np.uint32))
+    np.testing.assert_allclose(probs, p[order], rtol=1e-12)
+
+
+# -------------------------------------------------------------------- mask
+def test_apply_mask_bit_order(oracle):
+    """id t is allowed iff bit (t & 31) of word t >> 5 is set."""
+    words = np.array([0b1010, 1 << 31, 0x1], np.uint32)
+    x = np.arange(70, dtype=np.float32)
+    out = oracle.apply_mask(x, words)
+    allowed = np.nonzero(np.isfinite(out))[0].tolist()
+    assert allowed == [1, 3, 63, 64]
