@@ -38,7 +38,22 @@ def parse():
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic.md"),
                     help="rocprofv3 counter summary giving HBM bytes per launch")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a plain device copy of known size (counter calibration)")
     return ap.parse_args()
+
+
+def copy_calibration(nbytes: int = 256 * 2**20, reps: int = 8):
+    """A plain copy of known size: FETCH_SIZE / WRITE_SIZE per dispatch read
+    against `nbytes` give the scale factor applied to the sampling kernel."""
+    import torch
+
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").uniform_()
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": nbytes, "reps": reps}), flush=True)
 
 
 def read_traffic(path: str, kernel: str, workload: str):
@@ -55,6 +70,9 @@ def read_traffic(path: str, kernel: str, workload: str):
 
 def main():
     args = parse()
+    if args.copy_calibration:
+        copy_calibration()
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py: this build runs on one GPU only (the sampling path is row-parallel; "
