@@ -7,7 +7,7 @@ namespace zi {
 
 // Limits shared by the host planner and the kernels.
 constexpr int kThreadsHost = 256;   // threads per workgroup
-constexpr int kMaxGHost = 16;       // chunks per row
+constexpr int kMaxGHost = 16;        // chunks per row
 constexpr int kCapAHost = 256;      // candidates one chunk may publish
 constexpr int kMaxChunkElems = 16384;
 constexpr int kMaxVocab = kMaxGHost * kMaxChunkElems;  // 262144

@@ -189,6 +189,14 @@ __device__ __forceinline__ float pen_apply(float v, uint32_t cnt, float delta, c
 }
 
 // ------------------------------------------------------------ the stream
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+// Logits are read exactly once: non-temporal loads keep them from displacing
+// anything useful in the caches.
+__device__ __forceinline__ uint4 ld_stream(const uint4 *p) {
+    u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+    return make_uint4(t.x, t.y, t.z, t.w);
+}
+
 template <typename T, int NV>
 struct ChunkRegs {
     static constexpr int VEC = VecTraits<T>::VEC;
@@ -231,7 +239,7 @@ __device__ __forceinline__ float chunk_stream(const RowSource &a, int row, int c
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         int q = min(j * kThreads + tid, nvec - 1);
-        raw[j] = *reinterpret_cast<const uint4 *>(base + q * VEC);
+        raw[j] = ld_stream(reinterpret_cast<const uint4 *>(base + q * VEC));
         if (HAS_MASK) mw[j] = mrow[(c0 + q * VEC) >> 5];
     }
     uint32_t pw[NV];
@@ -638,68 +646,64 @@ struct MergeLds {
 __device__ __forceinline__ int row_merge(const uint64_t *g_key, const float *g_val, const int32_t *g_cnt, int row,
                                          int G, int k, MergeLds &ml, uint64_t *okey, float *oval) {
     const int tid = threadIdx.x;
-    constexpr int kPer = (kMaxG * kCapA) / kThreads;  // slots per thread (max)
-    uint64_t kk[kPer];
-    float vv[kPer];
     const int slots = G * k;
     const int64_t rb = (int64_t)row * G;
+    // one round trip: every slot of every list is requested before any is used
     int cn = 0;
     if (tid < G) cn = ld_agent(&g_cnt[rb + tid]);
+    for (int s0 = 0; s0 < slots; s0 += 4 * kThreads) {
+        uint64_t kk[4];
+        float vv[4];
 #pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-        int s = tid + u * kThreads;
-        if (s < slots) {
-            int g = s / k, i = s - g * k;
-            kk[u] = ld_agent(&g_key[(rb + g) * kCapA + i]);
-            vv[u] = ld_agent(&g_val[(rb + g) * kCapA + i]);
+        for (int u = 0; u < 4; ++u) {
+            int s = s0 + u * kThreads + tid;
+            if (s < slots) {
+                int g = s / k, i = s - g * k;
+                kk[u] = ld_agent(&g_key[(rb + g) * kCapA + i]);
+                vv[u] = ld_agent(&g_val[(rb + g) * kCapA + i]);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            int s = s0 + u * kThreads + tid;
+            if (s < slots) {
+                int g = s / k, i = s - g * k;
+                ml.key[g][i] = kk[u];
+                ml.val[g][i] = vv[u];
+            }
         }
     }
     if (tid < G) ml.cnt[tid] = cn;
-#pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-        int s = tid + u * kThreads;
-        if (s < slots) {
-            int g = s / k, i = s - g * k;
-            ml.key[g][i] = kk[u];
-            ml.val[g][i] = vv[u];
-        }
-    }
     __syncthreads();
     int total = 0;
     for (int g = 0; g < G; ++g) total += ml.cnt[g];
     const int need = min(k, total);
     int half = 1;
     while (half * 2 <= k) half *= 2;  // largest power of two <= k
-#pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-        int s = tid + u * kThreads;
-        if (s >= slots) continue;
-        int g = s / k, i = s - g * k;
-        if (i >= ml.cnt[g]) continue;
-        const uint64_t mine = ml.key[g][i];
-        // pos[h] = number of entries of list h greater than mine, found by a
-        // branch-free power-of-two search advanced for all lists in lock-step
-        int pos[kMaxG];
-        int len[kMaxG];
+    // rank of entry (g, i) = i + sum over other lists of the entries greater
+    // than it, by branch-free power-of-two searches advanced for every list in
+    // lock-step (their LDS reads are independent and issue together)
+    for (int s = tid; s < slots; s += kThreads) {
+        const int g = s / k, i = s - g * k;
+        const bool live = i < ml.cnt[g];
+        const uint64_t mine = ml.key[g][min(i, kCapA - 1)];
+        int pos[kMaxG], len[kMaxG];
 #pragma unroll
         for (int h = 0; h < kMaxG; ++h) {
             pos[h] = 0;
             len[h] = (h < G && h != g) ? ml.cnt[h] : 0;
         }
         for (int st = half; st > 0; st >>= 1) {
+            uint64_t kv[kMaxG];
 #pragma unroll
-            for (int h = 0; h < kMaxG; ++h) {
-                if (h < G) {
-                    const int probe = pos[h] + st;
-                    const uint64_t kv = ml.key[h][min(probe, kCapA) - 1];
-                    pos[h] += (probe <= len[h] && kv > mine) ? st : 0;
-                }
-            }
+            for (int h = 0; h < kMaxG; ++h) kv[h] = ml.key[h][max(min(pos[h] + st, len[h]) - 1, 0)];
+#pragma unroll
+            for (int h = 0; h < kMaxG; ++h) pos[h] += (pos[h] + st <= len[h] && kv[h] > mine) ? st : 0;
         }
         int rank = i;
 #pragma unroll
         for (int h = 0; h < kMaxG; ++h) rank += pos[h];
-        if (rank < need) {
+        if (live && rank < need) {
             okey[rank] = mine;
             oval[rank] = ml.val[g][i];
         }
