@@ -95,6 +95,8 @@ extern "C" int32_t zi_create(zi_ctx **out, int32_t device, int32_t max_rows, int
         {(void **)&c->g_raw, R * G * 16 * sizeof(uint32_t)},
         {(void **)&c->g_top2, R * G * 2 * sizeof(float)},
         {(void **)&c->g_tail, R * 16 * sizeof(float)},
+        {(void **)&c->win_ids, R * zi::kMaxWinHost * sizeof(uint32_t)},
+        {(void **)&c->win_len, R * sizeof(int32_t)},
     };
     for (auto &b : bufs) {
         e = hipMalloc(b.p, b.bytes);
@@ -117,7 +119,8 @@ extern "C" void zi_destroy(zi_ctx *c) {
     if (!c) return;
     hipSetDevice(c->device);
     if (c->own_stream) hipStreamSynchronize(c->own_stream);
-    void *ptrs[] = {c->g_key, c->g_val, c->g_cnt, c->tickets, c->g_stat, c->g_cls, c->g_raw, c->g_top2, c->g_tail};
+    void *ptrs[] = {c->g_key, c->g_val,  c->g_cnt,  c->tickets, c->g_stat, c->g_cls,
+                    c->g_raw, c->g_top2, c->g_tail, c->win_ids, c->win_len};
     for (void *p : ptrs)
         if (p) hipFree(p);
     if (c->own_stream) hipStreamDestroy(c->own_stream);
@@ -139,15 +142,15 @@ extern "C" int32_t zi_sync(zi_ctx *c) {
 
 namespace zi {
 
-// Chunking: 256 threads x EPT elements per workgroup, EPT in {16, 32, 64};
-// the largest EPT that still gives >= 512 workgroups (or EPT 16), with at
-// most kMaxG chunks per row.
+// Chunking: 512 threads x EPT elements per workgroup, EPT in {16, 32, 64};
+// the largest EPT that still gives >= 256 workgroups (one per CU; or EPT 16),
+// with at most kMaxG chunks per row.
 Plan plan_rows(int rows, int V, int dtype) {
     Plan pl;
     const int vec = dtype == ZI_F32 ? 4 : 8;
     int ept = 64;
     auto chunks = [&](int e) { return (V + kThreadsHost * e - 1) / (kThreadsHost * e); };
-    while (ept > 16 && (int64_t)rows * chunks(ept) < 512 && chunks(ept / 2) <= kMaxGHost) ept /= 2;
+    while (ept > 16 && (int64_t)rows * chunks(ept) < 256 && chunks(ept / 2) <= kMaxGHost) ept /= 2;
     int G = chunks(ept);
     int CH = (V + G - 1) / G;
     CH = (CH + 63) / 64 * 64;
@@ -250,6 +253,14 @@ extern "C" int32_t zi_sample_rows(zi_ctx *c, const zi_params *p, const zi_batch 
     zi::RowSource src;
     rc = fill_source(b, p, true, src, pl, "zi_sample_rows");
     if (rc) return rc;
+    if (src.hist && src.hist_ld > zi::kMaxWinHost) {  // the kernels prefetch whole history rows
+        hipError_t e = zi::launch_window_compact(src.hist, src.hist_len, src.hist_ld, src.win, b->rows, c->win_ids,
+                                                 c->win_len, c->stream);
+        if (e != hipSuccess) return zi_hip_fail(e, "window compaction launch");
+        src.hist = c->win_ids;
+        src.hist_len = c->win_len;
+        src.hist_ld = zi::kMaxWinHost;
+    }
 
     if (p->temp <= 0.0f)  // greedy: argmax of the penalized row (src/sampler.zig:193)
         return run_argmax(c, src, b, pl, out->tok, out->margin, nullptr, nullptr, out->ndraws);

@@ -33,7 +33,6 @@ __device__ __forceinline__ void ref_step(float v, uint32_t id, float &best, floa
 template <bool P>
 struct ArgPenLds {
     PenTable pen;
-    FlagList fl;
 };
 template <>
 struct ArgPenLds<false> {};
@@ -57,21 +56,17 @@ __global__ __launch_bounds__(kThreads) void argmax_kernel(ArgmaxParams P) {
     const int c1 = min(a.V, c0 + a.CH);
     const int body_end = a.V & ~15;
 
-    RowPen rp = row_pen(a, row);
     PenTable *pen = nullptr;
-    FlagList *fl = nullptr;
-    if constexpr (HAS_PEN) {
-        pen = &pl.pen;
-        fl = &pl.fl;
-    }
+    if constexpr (HAS_PEN) pen = &pl.pen;
+    PenOwn own;
     if (tid < 16) {
         s_ck[tid] = 0ull;
         s_raw[tid] = 0x7FC00000u;
         s_tail[tid] = __builtin_nanf("");
     }
     ChunkRegs<T, NV> cr;
-    chunk_stream<T, NV, HAS_MASK, HAS_PEN>(a, row, c0, c1, cr, pen, fl, rp);
-    __syncthreads();  // s_* initialised, diverted list complete
+    chunk_stream<T, NV, HAS_MASK, HAS_PEN>(a, row, c0, c1, cr, pen, &own);
+    __syncthreads();  // s_* initialised
 
     // per-thread class records (thread t only meets classes (t*VEC + e) & 15)
     uint64_t ck[VEC];
@@ -96,16 +91,19 @@ __global__ __launch_bounds__(kThreads) void argmax_kernel(ArgmaxParams P) {
             }
         }
     }
-    // diverted (penalized) elements: one per thread
-    int nf = 0;
-    if constexpr (HAS_PEN) nf = fl->n;
-    for (int i = tid; i < nf; i += kThreads) {
-        uint32_t id;
-        float v = flag_value(a, *pen, *fl, rp, i, id);
-        if (v == v) {
-            if ((int)id < body_end) atomicMax(&s_ck[id & 15], (unsigned long long)ckey(v, id));
-            else s_tail[id - body_end] = v;
-            top2_merge(t1, t2, v, -INFINITY);
+    // penalized elements, each from its owner thread
+    if constexpr (HAS_PEN) {
+#pragma unroll
+        for (int u = 0; u < kOwnSlots; ++u) {
+            const uint32_t id = own.id[u];
+            if (id != 0xFFFFFFFFu) {
+                const float v = owned_value(a, *pen, own, u);
+                if (v == v) {
+                    if ((int)id < body_end) atomicMax(&s_ck[id & 15], (unsigned long long)ckey(v, id));
+                    else s_tail[id - body_end] = v;
+                    top2_merge(t1, t2, v, -INFINITY);
+                }
+            }
         }
     }
     // reduce records over lanes sharing the same classes, top-2 over the wave
@@ -143,10 +141,15 @@ __global__ __launch_bounds__(kThreads) void argmax_kernel(ArgmaxParams P) {
                 s_raw[cls0 + e] = __float_as_uint(x);
         }
     }
-    for (int i = tid; i < nf; i += kThreads) {
-        uint32_t id;
-        float v = flag_value(a, *pen, *fl, rp, i, id);
-        if ((int)id < body_end && v == v && ckey(v, id) == s_ck[id & 15]) s_raw[id & 15] = __float_as_uint(v);
+    if constexpr (HAS_PEN) {
+#pragma unroll
+        for (int u = 0; u < kOwnSlots; ++u) {
+            const uint32_t id = own.id[u];
+            if (id != 0xFFFFFFFFu) {
+                const float v = owned_value(a, *pen, own, u);
+                if ((int)id < body_end && v == v && ckey(v, id) == s_ck[id & 15]) s_raw[id & 15] = __float_as_uint(v);
+            }
+        }
     }
     __syncthreads();
     const int64_t rg = (int64_t)row * G + g;

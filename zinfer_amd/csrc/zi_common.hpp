@@ -3,9 +3,9 @@
 // Layout conventions used by every kernel:
 //  * One row of V logits is split into G chunks of CH elements (CH a multiple
 //    of 64); chunk g covers ids [g*CH, min(V, (g+1)*CH)) and is handled by one
-//    256-thread workgroup (4 wave64s).
+//    512-thread workgroup (8 wave64s).
 //  * Thread t of a workgroup loads NV 16-byte vectors: vector j holds the
-//    VEC = 16/sizeof(T) consecutive ids starting at c0 + (j*256 + t)*VEC, so
+//    VEC = 16/sizeof(T) consecutive ids starting at c0 + (j*512 + t)*VEC, so
 //    each wave's load instruction reads 1 KiB of contiguous memory.
 //  * Ordering keys: okey() maps a float to a uint32 whose unsigned order is
 //    the float order with -0 == +0; ckey() appends ~id so that larger 64-bit
@@ -17,7 +17,7 @@
 
 namespace zi {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
 constexpr uint32_t kNegInfKey = 0x007FFFFFu;  // okey(-inf)
 
@@ -51,15 +51,19 @@ __device__ __forceinline__ int lanes_below(uint64_t m) {
 
 __device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
 
-// Largest T such that at least r lanes of the wave hold key >= T (0 if fewer
-// than r lanes have a nonzero key).  32-step bisection on ballot counts; T is
-// wave-uniform.
-__device__ __forceinline__ uint32_t wave_kth_largest(uint32_t key, int r) {
+// Largest T such that at least r of the wave's keys (N per lane) are >= T
+// (0 if fewer than r keys are nonzero).  32-step bisection on ballot counts;
+// T is wave-uniform.
+template <int N>
+__device__ __forceinline__ uint32_t wave_kth_largest(const uint32_t (&key)[N], int r) {
     uint32_t T = 0;
 #pragma unroll
     for (int b = 31; b >= 0; --b) {
-        uint32_t cand = T | (1u << b);
-        if (__popcll(ballot(key >= cand)) >= r) T = cand;
+        const uint32_t cand = T | (1u << b);
+        int c = 0;
+#pragma unroll
+        for (int i = 0; i < N; ++i) c += __popcll(ballot(key[i] >= cand));
+        if (c >= r) T = cand;
     }
     return T;
 }
@@ -94,6 +98,59 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
     uint32_t lo = __shfl_xor((uint32_t)v, m), hi = __shfl_xor((uint32_t)(v >> 32), m);
     return ((uint64_t)hi << 32) | lo;
 }
+
+// Value of `v` held by lane (this lane XOR D), D a power of two below 64,
+// without going through LDS: quad_perm DPP for 1 and 2, row shifts for 4,
+// row_ror:8 for 8, and the gfx950 permlane swaps for 16 and 32.
+template <int D>
+__device__ __forceinline__ uint32_t lane_xor(uint32_t v) {
+    static_assert(D == 1 || D == 2 || D == 4 || D == 8 || D == 16 || D == 32, "lane_xor distance");
+    if constexpr (D == 1) {
+        return __builtin_amdgcn_update_dpp(0u, v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+    } else if constexpr (D == 2) {
+        return __builtin_amdgcn_update_dpp(0u, v, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+    } else if constexpr (D == 4) {
+        const uint32_t up = __builtin_amdgcn_update_dpp(0u, v, 0x104, 0xF, 0xF, false);  // lane + 4
+        const uint32_t dn = __builtin_amdgcn_update_dpp(0u, v, 0x114, 0xF, 0xF, false);  // lane - 4
+        return (lane_id() & 4) ? dn : up;
+    } else if constexpr (D == 8) {
+        return __builtin_amdgcn_update_dpp(0u, v, 0x128, 0xF, 0xF, false);  // row_ror:8
+    } else if constexpr (D == 16) {
+        // r[0] = rows (0,0,2,2), r[1] = rows (1,1,3,3) of v
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return (lane_id() & 16) ? r[0] : r[1];
+    } else {
+        // r[0] = halves (lo,lo), r[1] = halves (hi,hi) of v
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return (lane_id() & 32) ? r[0] : r[1];
+    }
+}
+
+// Bitonic sort of one 32-bit key per lane, descending over the wave (all 64
+// lanes active); every exchange is a DPP / permlane move.
+template <int D, int SIZE>
+__device__ __forceinline__ uint32_t sort_step_u32(uint32_t x) {
+    const int lane = lane_id();
+    const uint32_t p = lane_xor<D>(x);
+    const bool keep_max = ((lane & D) == 0) == ((lane & SIZE) == 0);
+    return keep_max ? max(x, p) : min(x, p);
+}
+
+template <int D, int SIZE>
+__device__ __forceinline__ uint32_t sort_clean_u32(uint32_t x) {
+    x = sort_step_u32<D, SIZE>(x);
+    if constexpr (D > 1) x = sort_clean_u32<D / 2, SIZE>(x);
+    return x;
+}
+
+template <int SIZE>
+__device__ __forceinline__ uint32_t sort_from_u32(uint32_t x) {
+    x = sort_clean_u32<SIZE / 2, SIZE>(x);
+    if constexpr (SIZE < 64) x = sort_from_u32<SIZE * 2>(x);
+    return x;
+}
+
+__device__ __forceinline__ uint32_t wave_sort_desc_u32(uint32_t x) { return sort_from_u32<2>(x); }
 
 template <typename T>
 struct VecTraits;

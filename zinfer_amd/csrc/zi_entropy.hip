@@ -71,8 +71,7 @@ __global__ __launch_bounds__(kThreads) void entropy_kernel(EntropyParams P) {
         EntStageB b;
     } sm;
     __shared__ uint32_t s_bins[256];
-    __shared__ uint32_t s_tau[kWaves];
-    __shared__ int s_wcnt[kWaves];
+    __shared__ uint32_t s_tau[1];
     __shared__ int s_dig[2];
     __shared__ int s_n, s_flag;
     __shared__ float s_wmax[kWaves];
@@ -88,11 +87,10 @@ __global__ __launch_bounds__(kThreads) void entropy_kernel(EntropyParams P) {
     const int c1 = min(a.V, c0 + a.CH);
     const int k = P.k;
 
-    RowPen rp{};
     ChunkRegs<T, NV> cr;
     float ref = -INFINITY, S = 0.0f, U = 0.0f;
-    float tmax = chunk_stream<T, NV, false, false, EntHook>(a, row, c0, c1, cr, nullptr, nullptr, rp,
-                                                            EntHook{&ref, &S, &U});
+    chunk_stream<T, NV, false, false, EntHook>(a, row, c0, c1, cr, nullptr, nullptr,
+                                               EntHook{&ref, &S, &U});
 
     // workgroup merge of (ref, S, U) in f64
     float wm = wave_max_f(ref);
@@ -117,8 +115,7 @@ __global__ __launch_bounds__(kThreads) void entropy_kernel(EntropyParams P) {
 
     const int64_t rg = (int64_t)row * G + g;
     ChunkOut out{P.g_key + rg * kCapA, P.g_val + rg * kCapA, P.g_cnt + rg};
-    chunk_select_publish<T, NV, false>(a, rp, cr, tmax, c0, k, sm.a.sel, nullptr, nullptr, s_tau, s_wcnt, &s_n,
-                                       s_bins, s_dig, out);
+    chunk_select_publish<T, NV, false>(a, cr, c0, k, sm.a.sel, nullptr, nullptr, s_tau, &s_n, s_bins, s_dig, out);
     if (tid == 0) {
         double ts = 0.0, tu = 0.0;
         for (int w = 0; w < kWaves; ++w) {
@@ -229,6 +226,26 @@ hipError_t launch_mask(const MaskParams &P, hipStream_t st) {
         hipLaunchKernelGGL(mask_kernel<float>, dim3((unsigned)blocks), dim3(kThreads), 0, st, P);
     else
         hipLaunchKernelGGL(mask_kernel<uint16_t>, dim3((unsigned)blocks), dim3(kThreads), 0, st, P);
+    return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void window_compact_kernel(const uint32_t *hist, const int32_t *hist_len,
+                                                               int hist_ld, int win, uint32_t *out,
+                                                               int32_t *out_len) {
+    const int row = blockIdx.x;
+    int hl = hist_len[row];
+    hl = hl < 0 ? 0 : (hl > hist_ld ? hist_ld : hl);
+    const int nw = hl < win ? hl : win;
+    const uint32_t *src = hist + (int64_t)row * hist_ld + (hl - nw);
+    for (int i = threadIdx.x; i < nw; i += 256) out[(int64_t)row * kMaxWinHost + i] = src[i];
+    if (threadIdx.x == 0) out_len[row] = nw;
+}
+
+hipError_t launch_window_compact(const uint32_t *hist, const int32_t *hist_len, int hist_ld, int win, int rows,
+                                 uint32_t *out, int32_t *out_len, hipStream_t st) {
+    if (win > kMaxWinHost) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(window_compact_kernel, dim3(rows), dim3(256), 0, st, hist, hist_len, hist_ld, win, out,
+                       out_len);
     return hipGetLastError();
 }
 

@@ -21,6 +21,8 @@ struct zi_ctx {
     uint32_t *g_raw = nullptr;
     float *g_top2 = nullptr;
     float *g_tail = nullptr;
+    uint32_t *win_ids = nullptr;  // [max_rows][kMaxWinHost] compacted penalty windows
+    int32_t *win_len = nullptr;   // [max_rows]
 };
 
 int32_t zi_fail(int32_t code, const char *fmt, ...);

@@ -6,10 +6,10 @@
 namespace zi {
 
 // Limits shared by the host planner and the kernels.
-constexpr int kThreadsHost = 256;   // threads per workgroup
-constexpr int kMaxGHost = 16;        // chunks per row
+constexpr int kThreadsHost = 512;   // threads per workgroup (8 wave64s)
+constexpr int kMaxGHost = 8;        // chunks per row
 constexpr int kCapAHost = 256;      // candidates one chunk may publish
-constexpr int kMaxChunkElems = 16384;
+constexpr int kMaxChunkElems = 32768;
 constexpr int kMaxVocab = kMaxGHost * kMaxChunkElems;  // 262144
 constexpr int kMaxWinHost = 1024;   // penalty window
 constexpr int kMaxEditsHost = 128;  // sparse edits per row
@@ -103,5 +103,9 @@ hipError_t launch_sample(const SampleParams &P, int dtype, int nv, int rows, hip
 hipError_t launch_argmax(const ArgmaxParams &P, int dtype, int nv, int rows, hipStream_t st);
 hipError_t launch_entropy(const EntropyParams &P, int dtype, int nv, int rows, hipStream_t st);
 hipError_t launch_mask(const MaskParams &P, hipStream_t st);
+// Copies each row's penalty window (the last min(hist_len, win) ids) to
+// out[row][0, nw) and nw to out_len[row] (rows with hist_ld > kMaxWinHost).
+hipError_t launch_window_compact(const uint32_t *hist, const int32_t *hist_len, int hist_ld, int win, int rows,
+                                 uint32_t *out, int32_t *out_len, hipStream_t st);
 
 }  // namespace zi

@@ -13,23 +13,26 @@
 // Hot-loop design: every load is issued unconditionally (addresses clamped
 // into the chunk) so the compiler waits per load and the transform overlaps
 // the stream; lanes past the chunk end become NaN (never selected, ignored by
-// fmaxf); penalized ids are rare, so they are pulled out of the stream into an
-// LDS side list and penalized after it.
+// fmaxf).  Penalized ids are rare: the stream only turns them into NaN, and
+// each distinct penalized id of the chunk has an owner thread that reloads its
+// logit while the stream is in flight and penalizes it after the stream.
 #pragma once
 #include "zi_common.hpp"
 #include "zi_launch.hpp"
 
 namespace zi {
 
-constexpr int kMaxCH = kMaxChunkElems;  // max chunk elements (256 threads x 64)
+constexpr int kMaxCH = kMaxChunkElems;  // max chunk elements (512 threads x 64)
 constexpr int kHashMax = 2048;          // LDS hash slots (window + edits <= 1152 ids)
 constexpr int kMaxWin = kMaxWinHost;    // max penalty window
 constexpr int kMaxEdits = kMaxEditsHost;
 constexpr int kCapA = kCapAHost;        // published candidates per chunk (>= top-k)
 constexpr int kMaxG = kMaxGHost;        // max chunks per row (V <= 262144)
 constexpr int kWaveCap = 256;           // stage-A candidates one wave may hold
-constexpr int kFlagMax = kMaxWin + kMaxEdits;
+constexpr int kWinPerThread = kMaxWin / kThreads;
+constexpr int kOwnSlots = kWinPerThread + 1;  // window ids + one edit per thread
 static_assert(kThreads == kThreadsHost, "workgroup size");
+static_assert(kMaxWin + kMaxEdits <= kThreads * 4, "penalized entries fit the candidate buffer");
 
 // ------------------------------------------------ cross-workgroup handoff
 // Chunk results travel through device scratch with agent-scope relaxed
@@ -77,22 +80,16 @@ __device__ __forceinline__ int pen_insert(PenTable &t, uint32_t id, int hs_log2)
     uint32_t h = hash_slot(id, hs_log2);
     const uint32_t m = (1u << hs_log2) - 1;
     for (;;) {
-        uint32_t prev = atomicCAS(&t.key[h], 0u, id + 1);
+        const uint32_t prev = atomicCAS(&t.key[h], 0u, id + 1);
         if (prev == 0u || prev == id + 1) return (int)h;
         h = (h + 1) & m;
     }
 }
 
-__device__ __forceinline__ int pen_find(const PenTable &t, uint32_t id, int hs_log2) {
-    uint32_t h = hash_slot(id, hs_log2);
-    const uint32_t m = (1u << hs_log2) - 1;
-    while (t.key[h] != id + 1) h = (h + 1) & m;
-    return (int)h;
-}
-
 // Per-row window bounds: the last min(hist_len, win) entries of hist.
 struct RowPen {
-    const uint32_t *win_ptr;
+    const uint32_t *win_ptr;  // hist[row] + hl - nw
+    int hl;                   // history length (clamped to hist_ld)
     int nw;
     const uint32_t *eid;
     const float *edl;
@@ -104,10 +101,12 @@ struct RowPen {
 __device__ __forceinline__ RowPen row_pen(const RowSource &a, int row) {
     RowPen r;
     r.nw = 0;
+    r.hl = 0;
     r.win_ptr = nullptr;
     if (a.hist && (a.do_rep || a.do_fp) && a.win > 0) {
         int hl = a.hist_len[row];
         hl = hl < 0 ? 0 : (hl > a.hist_ld ? a.hist_ld : hl);
+        r.hl = hl;
         r.nw = hl < a.win ? hl : a.win;
         r.win_ptr = a.hist + (int64_t)row * a.hist_ld + (hl - r.nw);
     }
@@ -121,59 +120,128 @@ __device__ __forceinline__ RowPen row_pen(const RowSource &a, int row) {
         r.eid = a.edit_ids + (int64_t)row * a.edit_ld;
         r.edl = a.edit_delta + (int64_t)row * a.edit_ld;
     }
-    int n = r.nw + r.ne;
-    int lg = 6;
-    while ((1 << lg) < 2 * n && lg < 11) ++lg;
-    r.hs_log2 = lg;
+    const int n = r.nw + r.ne;  // hash of >= 2n slots, 64 .. 2048 (no loop: keeps the load waits exact)
+    r.hs_log2 = n > 0 ? min(11, max(6, 32 - __clz(2 * n - 1))) : 6;
     r.any = n > 0;
     return r;
 }
 
 struct PenRegs {
-    uint32_t w[kMaxWin / kThreads];
+    uint32_t w[kWinPerThread];
     uint32_t e;
     float d;
 };
 
-__device__ __forceinline__ void pen_fetch(const RowPen &rp, PenRegs &pr) {
+// Penalty inputs, issued before the row's loads so that waiting for them
+// never waits for the row: the whole history row (hist_ld <= kMaxWin: lane
+// slot i = tid + u*kThreads holds hist[row][i]; the host compacts longer rows
+// to their windows first) and the first kMaxEdits edits, none of which needs
+// hist_len / edit_count.
+__device__ __forceinline__ void pen_prefetch(const RowSource &a, int row, PenRegs &pr) {
     const int tid = threadIdx.x;
+    const bool on = a.hist && (a.do_rep || a.do_fp) && a.win > 0;
+    const uint32_t *h = a.hist + (int64_t)row * a.hist_ld;
 #pragma unroll
-    for (int u = 0; u < kMaxWin / kThreads; ++u) {
-        int i = tid + u * kThreads;
-        pr.w[u] = (i < rp.nw) ? rp.win_ptr[i] : 0xFFFFFFFFu;
+    for (int u = 0; u < kWinPerThread; ++u) {
+        const int i = tid + u * kThreads;
+        pr.w[u] = (on && i < a.hist_ld) ? h[i] : 0xFFFFFFFFu;
     }
-    pr.e = (tid < rp.ne) ? rp.eid[tid] : 0xFFFFFFFFu;
-    pr.d = (tid < rp.ne) ? rp.edl[tid] : 0.0f;
+    const bool ed = a.edit_ids && tid < min(a.edit_ld, kMaxEdits);
+    pr.e = ed ? a.edit_ids[(int64_t)row * a.edit_ld + tid] : 0xFFFFFFFFu;
+    pr.d = ed ? a.edit_delta[(int64_t)row * a.edit_ld + tid] : 0.0f;
 }
 
-// Builds the chunk's bitset of penalized/edited ids and the id -> (count,
-// delta) hash.  Contains barriers: call from all threads.
-__device__ __forceinline__ void pen_build(PenTable &t, const RowPen &rp, const PenRegs &pr, int c0, int c1) {
+// Restricts the prefetched inputs to the window [hl - nw, hl) and the edit count.
+__device__ __forceinline__ void pen_window(const RowPen &rp, PenRegs &pr) {
     const int tid = threadIdx.x;
-    const int hs = 1 << rp.hs_log2;
+#pragma unroll
+    for (int u = 0; u < kWinPerThread; ++u) {
+        const int i = tid + u * kThreads;
+        pr.w[u] = (i >= rp.hl - rp.nw && i < rp.hl) ? pr.w[u] : 0xFFFFFFFFu;
+    }
+    if (tid >= rp.ne) {
+        pr.e = 0xFFFFFFFFu;
+        pr.d = 0.0f;
+    }
+}
+
+// The penalized ids this thread owns (first inserter of each distinct id of
+// the chunk), their hash slots and their logits with the mask applied.
+struct PenOwn {
+    uint32_t id[kOwnSlots];  // 0xFFFFFFFF: none
+    int slot[kOwnSlots];
+    float x[kOwnSlots];
+};
+
+template <typename T>
+__device__ __forceinline__ float load_logit(const T *row, uint32_t id);
+template <>
+__device__ __forceinline__ float load_logit<float>(const float *row, uint32_t id) {
+    return row[id];
+}
+template <>
+__device__ __forceinline__ float load_logit<uint16_t>(const uint16_t *row, uint32_t id) {
+    return __uint_as_float((uint32_t)row[id] << 16);
+}
+
+// Clears the chunk's bitset and the whole hash (no dependence on the row's
+// window size, so it runs while the row streams; the caller's next barrier
+// orders it before the inserts).
+__device__ __forceinline__ void pen_clear(PenTable &t, int c0, int c1) {
+    const int tid = threadIdx.x;
     const int nbw = (c1 - c0 + 31) >> 5;
     for (int i = tid; i < nbw; i += kThreads) t.bits[i] = 0u;
-    for (int i = tid; i < hs; i += kThreads) {
+    for (int i = tid; i < kHashMax; i += kThreads) {
         t.key[i] = 0u;
         t.cnt[i] = 0u;
         t.delta[i] = 0.0f;
     }
-    __syncthreads();
+}
+
+// Marks the chunk's penalized/edited ids in the bitset; the thread whose
+// atomicOr set an id's bit owns that id and issues the reload of its logit
+// (row = logits row, mrow = mask row or null).  No barrier.
+template <typename T>
+__device__ __forceinline__ void pen_mark(PenTable &t, const PenRegs &pr, int c0, int c1, PenOwn &own, const T *row,
+                                         const uint32_t *mrow) {
 #pragma unroll
-    for (int u = 0; u < kMaxWin / kThreads; ++u) {
-        uint32_t id = pr.w[u];
+    for (int u = 0; u < kOwnSlots; ++u) {
+        const uint32_t id = u < kWinPerThread ? pr.w[u] : pr.e;
+        own.id[u] = 0xFFFFFFFFu;
+        own.x[u] = 0.0f;
         if (id >= (uint32_t)c0 && id < (uint32_t)c1) {
-            int h = pen_insert(t, id, rp.hs_log2);
+            const uint32_t b = 1u << ((id - c0) & 31);
+            if (!(atomicOr(&t.bits[(id - c0) >> 5], b) & b)) own.id[u] = id;
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < kOwnSlots; ++u) {
+        if (own.id[u] != 0xFFFFFFFFu) {
+            float v = load_logit<T>(row, own.id[u]);
+            if (mrow && !((mrow[own.id[u] >> 5] >> (own.id[u] & 31)) & 1u)) v = -INFINITY;
+            own.x[u] = v;
+        }
+    }
+}
+
+// Fills the id -> (count, delta) hash and the owners' slots.  No barrier:
+// owners read their entries after the caller's next barrier.
+__device__ __forceinline__ void pen_count(PenTable &t, const RowPen &rp, const PenRegs &pr, int c0, int c1,
+                                          PenOwn &own) {
+#pragma unroll
+    for (int u = 0; u < kWinPerThread; ++u) {
+        const uint32_t id = pr.w[u];
+        if (id >= (uint32_t)c0 && id < (uint32_t)c1) {
+            const int h = pen_insert(t, id, rp.hs_log2);
             atomicAdd(&t.cnt[h], 1u);
-            atomicOr(&t.bits[(id - c0) >> 5], 1u << ((id - c0) & 31));
+            if (own.id[u] == id) own.slot[u] = h;
         }
     }
     if (pr.e >= (uint32_t)c0 && pr.e < (uint32_t)c1) {
-        int h = pen_insert(t, pr.e, rp.hs_log2);
+        const int h = pen_insert(t, pr.e, rp.hs_log2);
         t.delta[h] = pr.d;
-        atomicOr(&t.bits[(pr.e - c0) >> 5], 1u << ((pr.e - c0) & 31));
+        if (own.id[kWinPerThread] == pr.e) own.slot[kWinPerThread] = h;
     }
-    __syncthreads();
 }
 
 __device__ __forceinline__ float pen_apply(float v, uint32_t cnt, float delta, const RowSource &a) {
@@ -201,23 +269,18 @@ template <typename T, int NV>
 struct ChunkRegs {
     static constexpr int VEC = VecTraits<T>::VEC;
     float x[NV * VEC];
-    float m4[NV];  // per-vector maxima (NaN lanes ignored)
-    float m1;      // lane max (first occurrence), its id, and the lane's
-    uint32_t id1;  // second largest value (multiset), all kept as loads land
-    float m2;
+    float m4[NV];  // per-vector maxima (NaN lanes ignored; NaN if the vector holds no value)
+    float lmax;    // lane maximum (-inf if the lane holds no value)
 };
 
-struct FlagList {  // penalized / edited elements diverted from the stream
-    uint32_t id[kFlagMax];
-    float x[kFlagMax];
-    int n;
-};
-
-// Streams the chunk [c0, c1) of `row` into registers with the mask applied
-// and penalized ids diverted into `fl` (their register copies become NaN).
-// Returns the thread max (-inf if the thread holds no selectable value);
-// hook(j, v, max) sees each transformed vector as soon as its load lands.
-// HAS_PEN needs PenTable `t` and FlagList `fl` in LDS and contains barriers.
+// Streams the chunk [c0, c1) of `row` into registers with the mask applied;
+// penalized ids become NaN in registers (their owners in `own` carry them).
+// The penalty inputs are prefetched ahead of the row and the bitset of
+// penalized ids is built while the row's loads are in flight; the count/delta
+// hash is filled after the stream.  Returns the thread max (-inf if the thread
+// holds no selectable value); hook(j, v, max) sees each transformed vector as
+// soon as its load lands.  HAS_PEN needs PenTable `t` in LDS and contains
+// barriers.
 struct NoHook {
     template <int VEC>
     __device__ void operator()(int, const float (&)[VEC], float) const {}
@@ -225,7 +288,7 @@ struct NoHook {
 
 template <typename T, int NV, bool HAS_MASK, bool HAS_PEN, class Hook = NoHook>
 __device__ __forceinline__ float chunk_stream(const RowSource &a, int row, int c0, int c1, ChunkRegs<T, NV> &cr,
-                                              PenTable *t, FlagList *fl, const RowPen &rp, Hook hook = Hook()) {
+                                              PenTable *t, PenOwn *own, Hook hook = Hook()) {
     constexpr int VEC = VecTraits<T>::VEC;
     const int tid = threadIdx.x;
     const int nvec = (c1 - c0 + VEC - 1) / VEC;
@@ -233,7 +296,8 @@ __device__ __forceinline__ float chunk_stream(const RowSource &a, int row, int c
     const uint32_t *mrow = HAS_MASK ? a.mask + (int64_t)row * a.mask_ld : nullptr;
 
     PenRegs pr;
-    if (HAS_PEN) pen_fetch(rp, pr);  // issued first: waiting for these does not wait for the row
+    if (HAS_PEN) pen_prefetch(a, row, pr);
+    // the row's loads depend on nothing that waits for memory
     uint4 raw[NV];
     uint32_t mw[NV];
 #pragma unroll
@@ -243,19 +307,18 @@ __device__ __forceinline__ float chunk_stream(const RowSource &a, int row, int c
         if (HAS_MASK) mw[j] = mrow[(c0 + q * VEC) >> 5];
     }
     uint32_t pw[NV];
+    RowPen rp;
     if (HAS_PEN) {
-        if (tid == 0) fl->n = 0;
-        pen_build(*t, rp, pr, c0, c1);
+        pen_clear(*t, c0, c1);
+        rp = row_pen(a, row);
+        pen_window(rp, pr);
+        __syncthreads();  // tables cleared
+        pen_mark<T>(*t, pr, c0, c1, *own, reinterpret_cast<const T *>(a.logits) + (int64_t)row * a.ld, mrow);
+        __syncthreads();  // bitset complete
 #pragma unroll
-        for (int j = 0; j < NV; ++j) {
-            int q = min(j * kThreads + tid, nvec - 1);
-            pw[j] = t->bits[(q * VEC) >> 5];
-        }
+        for (int j = 0; j < NV; ++j) pw[j] = t->bits[(min(j * kThreads + tid, nvec - 1) * VEC) >> 5];
     }
     float tmax = -INFINITY;
-    cr.m1 = -INFINITY;
-    cr.m2 = -INFINITY;
-    cr.id1 = 0xFFFFFFFFu;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const int q = j * kThreads + tid;
@@ -268,17 +331,10 @@ __device__ __forceinline__ float chunk_stream(const RowSource &a, int row, int c
             for (int e = 0; e < VEC; ++e) v[e] = ((mb >> e) & 1u) ? v[e] : -INFINITY;
         }
         if (HAS_PEN) {
-            uint32_t pb = (pw[j] >> ((q * VEC) & 31)) & ((1u << VEC) - 1u);
-            if (pb && id0 < c1) {
+            const uint32_t pb = (pw[j] >> ((q * VEC) & 31)) & ((1u << VEC) - 1u);
+            if (pb) {
 #pragma unroll
-                for (int e = 0; e < VEC; ++e) {
-                    if ((pb >> e) & 1u) {
-                        int s = atomicAdd(&fl->n, 1);
-                        fl->id[s] = (uint32_t)(id0 + e);
-                        fl->x[s] = v[e];
-                        v[e] = __builtin_nanf("");
-                    }
-                }
+                for (int e = 0; e < VEC; ++e) v[e] = ((pb >> e) & 1u) ? __builtin_nanf("") : v[e];
             }
         }
         const int lim = c1 - id0;
@@ -291,92 +347,87 @@ __device__ __forceinline__ float chunk_stream(const RowSource &a, int row, int c
 #pragma unroll
         for (int e = 1; e < VEC; ++e) m = fmaxf(m, v[e]);
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-            cr.x[j * VEC + e] = v[e];
-            const bool gt = v[e] > cr.m1;  // strict: the first (lowest id) maximum stays
-            cr.m2 = gt ? cr.m1 : fmaxf(cr.m2, v[e]);
-            cr.id1 = gt ? (uint32_t)(id0 + e) : cr.id1;
-            cr.m1 = gt ? v[e] : cr.m1;
-        }
+        for (int e = 0; e < VEC; ++e) cr.x[j * VEC + e] = v[e];
         cr.m4[j] = m;
         tmax = fmaxf(tmax, m);
         hook.template operator()<VEC>(j, v, m);
     }
+    if (HAS_PEN) pen_count(*t, rp, pr, c0, c1, *own);  // read by owners after the caller's next barrier
+    cr.lmax = tmax;
     return tmax;
 }
 
-// Penalized value of diverted entry i (call after a barrier that follows
+// Penalized value of owned entry u (call after a barrier that follows
 // chunk_stream).
-__device__ __forceinline__ float flag_value(const RowSource &a, const PenTable &t, const FlagList &fl,
-                                            const RowPen &rp, int i, uint32_t &id) {
-    id = fl.id[i];
-    int h = pen_find(t, id, rp.hs_log2);
-    return pen_apply(fl.x[i], t.cnt[h], t.delta[h], a);
+__device__ __forceinline__ float owned_value(const RowSource &a, const PenTable &t, const PenOwn &own, int u) {
+    const int h = own.slot[u];
+    return pen_apply(own.x[u], t.cnt[h], t.delta[h], a);
 }
 
 // --------------------------------------------------------- stage A select
-// Candidate threshold: each wave takes the ceil(k/4)-th largest of its lanes'
-// maxima; the minimum over the 4 waves is <= the k-th largest value the
-// stream kept (each wave owns ceil(k/4) distinct values at or above it), so
-// every element of the chunk's top-k that the stream kept passes, and every
-// diverted (penalized) element above it is added separately.  Returns tau
-// (-inf when some wave has too few values).
-__device__ __forceinline__ float chunk_tau(float tmax, int k, uint32_t *s_tau) {
-    const int tid = threadIdx.x;
-    uint32_t mkey = (tmax == tmax) ? okey(tmax) : 0u;
-    int r = (k + kWaves - 1) / kWaves;
-    uint32_t tw = wave_kth_largest(mkey, r);
-    if ((tid & 63) == 0) s_tau[tid >> 6] = tw;
+// Candidate threshold tau <= the chunk's k-th largest value.  Each wave sorts
+// its 64 lane maxima (distinct elements of the chunk) and contributes its r
+// largest, r = max(ceil(k/W), 64/W); the union holds W*r >= k elements, so its
+// k-th largest is a lower bound of the chunk's k-th largest.  Lanes without a
+// value contribute okey(-inf) (harmless: a bound at -inf admits everything).
+// Penalized elements diverted from the stream are not in the union, which
+// only lowers the bound.  Contains two barriers.
+constexpr int kMaxR = kMaxTopK / kWaves;  // r for the largest k
+static_assert(kMaxR <= 64, "one sorted wave supplies r keys");
+
+__device__ __forceinline__ float chunk_tau(float m1, int k, uint32_t *uni, uint32_t *s_tau) {
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int r = max((k + kWaves - 1) / kWaves, 64 / kWaves);
+    const uint32_t key = wave_sort_desc_u32((m1 == m1) ? okey(m1) : 0u);
+    if (lane < r) uni[wid * r + lane] = key;
     __syncthreads();
-    uint32_t tau = s_tau[0];
+    if (wid == 0) {
+        const int U = kWaves * r;
+        uint32_t t;
+        if (U <= 64) {
+            const uint32_t u = wave_sort_desc_u32(lane < U ? uni[lane] : 0u);
+            t = (uint32_t)__builtin_amdgcn_readlane((int)u, k - 1);
+        } else {
+            uint32_t u4[4];
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) tau = min(tau, s_tau[w]);
-    return (tau > kNegInfKey) ? okey_inv(tau) : -INFINITY;
+            for (int c = 0; c < 4; ++c) u4[c] = (lane + 64 * c < U) ? uni[lane + 64 * c] : 0u;
+            t = wave_kth_largest<4>(u4, k);
+        }
+        if (lane == 0) *s_tau = t;
+    }
+    __syncthreads();
+    const uint32_t t = *s_tau;
+    return t ? okey_inv(t) : -INFINITY;
 }
 
-// Appends this thread's elements >= tau to its wave's LDS region (keys/vals,
-// capacity wcap) by ballot compaction (no atomics); returns the wave's count,
-// which may exceed wcap (entries past it are dropped).  A lane whose second
-// largest value is below tau holds at most one candidate, its maximum, which
-// the stream already located; only lanes with two or more candidates scan
-// their vectors.
+// Stages every pair of register vectors whose maximum is >= tau into its
+// wave's LDS region (2*VEC values + the first id of each vector), by ballot
+// compaction over the NV/2 slots; returns the wave's count, which may exceed
+// `cap` (pairs past it are dropped).  A pair with no value has a NaN maximum
+// and is never staged.
 template <typename T, int NV>
-__device__ __forceinline__ int chunk_extract(const ChunkRegs<T, NV> &cr, int c0, float tau, uint64_t *keys,
-                                             float *vals, int wcap) {
+__device__ __forceinline__ int chunk_stage(const ChunkRegs<T, NV> &cr, int c0, float tau, float *sx, uint32_t *sid,
+                                           int cap) {
     constexpr int VEC = VecTraits<T>::VEC;
+    static_assert(NV % 2 == 0, "vectors are staged in pairs");
     const int tid = threadIdx.x;
-    const bool multi = cr.m2 >= tau;
-    const bool one = !multi && cr.m1 >= tau;
     int cnt = 0;
-    {
-        const uint64_t m = ballot(one);
-        const int pos = lanes_below(m);
-        if (one && pos < wcap) {
-            keys[pos] = ckey(cr.m1, cr.id1);
-            vals[pos] = cr.m1;
-        }
-        cnt = __popcll(m);
-    }
-    if (ballot(multi)) {
 #pragma unroll
-        for (int j = 0; j < NV; ++j) {
-            if (ballot(multi && cr.m4[j] >= tau)) {
-                const int id0 = c0 + (j * kThreads + tid) * VEC;
+    for (int j = 0; j < NV; j += 2) {
+        const bool p = fmaxf(cr.m4[j], cr.m4[j + 1]) >= tau;
+        const uint64_t b = ballot(p);
+        if (b) {
+            const int pos = cnt + lanes_below(b);
+            if (p && pos < cap) {
+                float4 *dst = reinterpret_cast<float4 *>(sx + pos * 2 * VEC);
 #pragma unroll
-                for (int e = 0; e < VEC; ++e) {
-                    const float x = cr.x[j * VEC + e];
-                    const bool p = multi && x >= tau;
-                    const uint64_t m = ballot(p);
-                    if (m) {
-                        const int pos = cnt + lanes_below(m);
-                        if (p && pos < wcap) {
-                            keys[pos] = ckey(x, (uint32_t)(id0 + e));
-                            vals[pos] = x;
-                        }
-                        cnt += __popcll(m);
-                    }
-                }
+                for (int q = 0; q < VEC / 2; ++q)
+                    dst[q] = make_float4(cr.x[j * VEC + 4 * q], cr.x[j * VEC + 4 * q + 1], cr.x[j * VEC + 4 * q + 2],
+                                         cr.x[j * VEC + 4 * q + 3]);
+                sid[2 * pos] = (uint32_t)(c0 + (j * kThreads + tid) * VEC);
+                sid[2 * pos + 1] = (uint32_t)(c0 + ((j + 1) * kThreads + tid) * VEC);
             }
+            cnt += __popcll(b);
         }
     }
     return cnt;
@@ -417,7 +468,7 @@ __device__ __forceinline__ uint64_t block_select(Src src, int need, uint32_t *bi
     uint64_t prefix = 0;
     int rem = need;
     for (int shift = 56;; shift -= 8) {
-        bins[tid] = 0u;
+        if (tid < 256) bins[tid] = 0u;
         __syncthreads();
         src(prefix, shift, bins);
         __syncthreads();
@@ -437,14 +488,6 @@ __device__ __forceinline__ void hist_add(uint64_t k, uint64_t prefix, int shift,
     bool match = (shift == 56) || ((k >> (shift + 8)) == (prefix >> (shift + 8)));
     if (match) atomicAdd(&bins[(k >> shift) & 255u], 1u);
 }
-
-struct LdsKeySrc {
-    const uint64_t *keys;
-    int n;
-    __device__ void operator()(uint64_t prefix, int shift, uint32_t *bins) const {
-        for (int i = threadIdx.x; i < n; i += kThreads) hist_add(keys[i], prefix, shift, bins);
-    }
-};
 
 template <typename T, int NV>
 struct RegKeySrc {
@@ -468,30 +511,6 @@ struct RegKeySrc {
     }
 };
 
-// Writes the keys (unique) of keys/vals[0..n) ranked by key descending to
-// okeys/ovals[rank] for rank < need.  One key per thread per round; the
-// comparisons read 16 keys per LDS round trip.
-__device__ __forceinline__ void rank_sort(const uint64_t *keys, const float *vals, int n, int need, uint64_t *okeys,
-                                          float *ovals) {
-    for (int i = threadIdx.x; i < n; i += kThreads) {
-        const uint64_t mine = keys[i];
-        int rank = 0;
-        int j = 0;
-        for (; j + 16 <= n; j += 16) {
-            uint64_t b[16];
-#pragma unroll
-            for (int u = 0; u < 16; ++u) b[u] = keys[j + u];
-#pragma unroll
-            for (int u = 0; u < 16; ++u) rank += (int)(b[u] > mine);
-        }
-        for (; j < n; ++j) rank += (int)(keys[j] > mine);
-        if (rank < need) {
-            okeys[rank] = mine;
-            ovals[rank] = vals[i];
-        }
-    }
-}
-
 // ------------------------------------------------------ stage A, complete
 // Scratch layout per (row, chunk): kCapA keys, kCapA values, one count.
 struct ChunkOut {
@@ -500,214 +519,264 @@ struct ChunkOut {
     int32_t *cnt;
 };
 
+constexpr int kSortMax = 256;  // candidates ranked without the radix-select path
+constexpr int kCandCap = kThreads * 4;
+constexpr int kStageCap = 32;  // staged vector pairs per wave
+
 template <typename T, int NV>
 struct SelectLds {
-    uint64_t wkey[kWaves][kWaveCap];  // wave-private candidate regions
-    float wval[kWaves][kWaveCap];
-    uint64_t ckey[kWaves * kWaveCap];  // gathered candidates
-    float cval[kWaves * kWaveCap];
-    uint64_t skey[kCapA];  // sorted top-k
+    static constexpr int VEC = VecTraits<T>::VEC;
+    uint32_t uni[kWaves * kMaxR];  // threshold union
+    float sx[kWaves][kStageCap * 2 * VEC];  // staged vector pairs
+    uint32_t sid[kWaves][kStageCap * 2];
+    uint64_t ckey[kCandCap];  // candidates
+    float cval[kCandCap];
+    uint64_t skey[kCapA];  // overflow path: the exact top-k, unsorted
     float sval[kCapA];
+    uint32_t rank[kSortMax];
+    int wcnt[kWaves];
 };
+
+// Ranks the n <= kSortMax unique keys by counting, split over the whole
+// workgroup: thread (b, i) counts the keys of block b greater than key i
+// (each wave reads the same block keys, so the reads are broadcasts), the
+// counts meet in rank[i] (zero on entry), and key i goes to out[rank] when
+// rank < k; slots [n, k) get key 0.  Contains a barrier.
+__device__ __forceinline__ void rank_publish(const uint64_t *keys, const float *vals, int n, int k,
+                                             uint32_t *rank, ChunkOut out) {
+    const int tid = threadIdx.x;
+    const int np = n <= 64 ? 64 : (n <= 128 ? 128 : 256);
+    const int nb = kThreads / np, bs = np / nb;
+    const int i = tid & (np - 1), b = tid / np;
+    if (i < n) {
+        const uint64_t mine = keys[i];
+        const int j0 = b * bs, j1 = min(j0 + bs, n);
+        uint32_t c = 0;
+        for (int j = j0; j < j1; ++j) c += (uint32_t)(keys[j] > mine);
+        if (c) atomicAdd(&rank[i], c);
+    }
+    __syncthreads();
+    if (tid < n) {
+        const uint32_t r = rank[tid];
+        if (r < (uint32_t)k) {
+            st_agent(&out.key[r], keys[tid]);
+            st_agent(&out.val[r], vals[tid]);
+        }
+    } else if (tid < k) {
+        st_agent(&out.key[tid], (uint64_t)0);  // padding: below every real key
+    }
+    if (tid == 0) st_agent(out.cnt, min(n, k));
+}
 
 // Stage A after chunk_stream: find the chunk's exact top-min(k, selectable)
 // sorted by (value desc, id asc), publish it to `out` (agent-scope stores).
-// LDS: `sl` (SelectLds), `t`/`fl` when HAS_PEN, small scalars.
+// LDS: `sl` (SelectLds), `t` when HAS_PEN (with the owners in `own`), small
+// scalars.
 template <typename T, int NV, bool HAS_PEN>
-__device__ __forceinline__ void chunk_select_publish(const RowSource &a, const RowPen &rp, ChunkRegs<T, NV> &cr,
-                                                     float tmax, int c0, int k, SelectLds<T, NV> &sl,
-                                                     PenTable *t, FlagList *fl, uint32_t *s_tau, int *s_wcnt,
-                                                     int *s_n, uint32_t *bins, int *s_dig, ChunkOut out) {
+__device__ __forceinline__ void chunk_select_publish(const RowSource &a, ChunkRegs<T, NV> &cr, int c0, int k,
+                                                     SelectLds<T, NV> &sl, const PenTable *t, const PenOwn *own,
+                                                     uint32_t *s_tau, int *s_n, uint32_t *bins, int *s_dig,
+                                                     ChunkOut out) {
+    constexpr int VEC = VecTraits<T>::VEC;
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-    const float tau = chunk_tau(tmax, k, s_tau);  // contains a barrier (fl->n final after it)
-    int wc = chunk_extract<T, NV>(cr, c0, tau, sl.wkey[wid], sl.wval[wid], kWaveCap);
-    if (lane == 0) s_wcnt[wid] = wc;
-    int nf = 0;
-    if (HAS_PEN) nf = fl->n;
+    if (tid == 0) *s_n = 0;
+    if (tid < kSortMax) sl.rank[tid] = 0u;
+    const float tau = chunk_tau(cr.lmax, k, sl.uni, s_tau);  // barriers: *s_n and rank settled
+    const int wc = chunk_stage<T, NV>(cr, c0, tau, sl.sx[wid], sl.sid[wid], kStageCap);
+    if (lane == 0) sl.wcnt[wid] = wc;
     __syncthreads();
     int off[kWaves + 1];
     off[0] = 0;
     bool overflow = false;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
-        overflow |= s_wcnt[w] > kWaveCap;
-        off[w + 1] = off[w] + min(s_wcnt[w], kWaveCap);
+        overflow |= sl.wcnt[w] > kStageCap;
+        off[w + 1] = off[w] + min(sl.wcnt[w], kStageCap);
     }
-    int n = off[kWaves];
-    // gather the wave regions contiguously, then the diverted entries >= tau
+    if (!overflow) {  // uniform
+        // expand the staged vectors: one element per thread
+        for (int q = tid; q < off[kWaves] * 2 * VEC; q += kThreads) {
+            const int v = q / (2 * VEC), e = q - v * (2 * VEC);
+            int w = 0;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w)
-        for (int i = tid; i < off[w + 1] - off[w]; i += kThreads) {
-            sl.ckey[off[w] + i] = sl.wkey[w][i];
-            sl.cval[off[w] + i] = sl.wval[w][i];
-        }
-    if (HAS_PEN) {
-        if (tid == 0) *s_n = n;
-        __syncthreads();
-        for (int i = tid; i < nf; i += kThreads) {
-            uint32_t id;
-            float v = flag_value(a, *t, *fl, rp, i, id);
-            if (v >= tau) {
-                int pos = atomicAdd(s_n, 1);
-                if (pos < kWaves * kWaveCap) {
-                    sl.ckey[pos] = ckey(v, id);
-                    sl.cval[pos] = v;
-                } else {
-                    overflow = true;
+            for (int i = 1; i < kWaves; ++i) w += (v >= off[i]);
+            int b = 0;
+#pragma unroll
+            for (int i = 1; i < kWaves; ++i) b = (w == i) ? off[i] : b;
+            const float x = sl.sx[w][(v - b) * 2 * VEC + e];
+            if (x >= tau) {
+                const int pos = atomicAdd(s_n, 1);
+                if (pos < kCandCap) {
+                    sl.ckey[pos] = ckey(x, sl.sid[w][2 * (v - b) + e / VEC] + (uint32_t)(e % VEC));
+                    sl.cval[pos] = x;
                 }
             }
         }
-        __syncthreads();
-        n = *s_n;
-        if (n > kWaves * kWaveCap) overflow = true;
     }
-    __syncthreads();
-    overflow = __syncthreads_or(overflow);
-    if (overflow) {
-        // More candidates than the buffers hold (clustered or tied values):
-        // exact radix select over registers + diverted entries, then rebuild.
-        uint64_t *extra = sl.skey;  // reuse: penalized keys (<= kFlagMax fits in ckey)
-        int ne = 0;
-        if (HAS_PEN) {
-            for (int i = tid; i < nf; i += kThreads) {
-                uint32_t id;
-                float v = flag_value(a, *t, *fl, rp, i, id);
-                sl.ckey[i] = ckey(v, id);
-                sl.cval[i] = v;
-            }
-            ne = nf;
-            __syncthreads();
-        }
-        (void)extra;
-        RegKeySrc<T, NV> src{&cr, c0, sl.ckey, ne};
-        uint64_t T0 = block_select(src, k, bins, s_dig);
-        if (tid == 0) *s_n = 0;
-        __syncthreads();
-        constexpr int VEC = VecTraits<T>::VEC;
-        // penalized entries first (they sit in ckey[0..ne)); collect into skey
+    if constexpr (HAS_PEN) {
+        if (!overflow) {
 #pragma unroll
-        for (int j = 0; j < NV; ++j) {
-            int e0 = c0 + (j * kThreads + tid) * VEC;
-#pragma unroll
-            for (int e = 0; e < VEC; ++e) {
-                float x = cr.x[j * VEC + e];
-                if (x == x) {
-                    uint64_t key = ckey(x, (uint32_t)(e0 + e));
-                    if (key >= T0) {
-                        int pos = atomicAdd(s_n, 1);
-                        if (pos < kCapA) {
-                            sl.skey[pos] = key;
-                            sl.sval[pos] = x;
+            for (int u = 0; u < kOwnSlots; ++u) {
+                if (own->id[u] != 0xFFFFFFFFu) {
+                    const float v = owned_value(a, *t, *own, u);
+                    if (v >= tau) {
+                        const int pos = atomicAdd(s_n, 1);
+                        if (pos < kCandCap) {
+                            sl.ckey[pos] = ckey(v, own->id[u]);
+                            sl.cval[pos] = v;
                         }
                     }
                 }
             }
         }
-        for (int i = tid; i < ne; i += kThreads) {
-            if (sl.ckey[i] >= T0) {
-                int pos = atomicAdd(s_n, 1);
-                if (pos < kCapA) {
-                    sl.skey[pos] = sl.ckey[i];
-                    sl.sval[pos] = sl.cval[i];
-                }
+    }
+    __syncthreads();
+    const int n = *s_n;
+    if (!overflow && n <= kSortMax) {  // uniform: read from LDS after the barrier
+        rank_publish(sl.ckey, sl.cval, n, k, sl.rank, out);
+        return;
+    }
+    // More candidates than the ranking takes (clustered or tied values):
+    // exact radix select over registers + penalized entries, then rank the top-k.
+    int ne = 0;
+    if constexpr (HAS_PEN) {
+        if (tid == 0) *s_n = 0;
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < kOwnSlots; ++u) {
+            if (own->id[u] != 0xFFFFFFFFu) {
+                const float v = owned_value(a, *t, *own, u);
+                const int q = atomicAdd(s_n, 1);  // < kMaxWin + kMaxEdits <= kCandCap
+                sl.ckey[q] = ckey(v, own->id[u]);
+                sl.cval[q] = v;
             }
         }
         __syncthreads();
-        n = min(*s_n, kCapA);
-        __syncthreads();
-        for (int i = tid; i < n; i += kThreads) {
-            sl.ckey[i] = sl.skey[i];
-            sl.cval[i] = sl.sval[i];
-        }
-        __syncthreads();
+        ne = *s_n;
     }
-    const int m = min(n, k);
-    rank_sort(sl.ckey, sl.cval, n, m, sl.skey, sl.sval);
+    RegKeySrc<T, NV> src{&cr, c0, sl.ckey, ne};
+    const uint64_t T0 = block_select(src, k, bins, s_dig);
+    if (tid == 0) *s_n = 0;
     __syncthreads();
-    for (int i = tid; i < m; i += kThreads) {
-        st_agent(&out.key[i], sl.skey[i]);
-        st_agent(&out.val[i], sl.sval[i]);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int e0 = c0 + (j * kThreads + tid) * VEC;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+            const float x = cr.x[j * VEC + e];
+            if (x == x) {
+                const uint64_t key = ckey(x, (uint32_t)(e0 + e));
+                if (key >= T0) {
+                    const int q = atomicAdd(s_n, 1);
+                    if (q < kCapA) {
+                        sl.skey[q] = key;
+                        sl.sval[q] = x;
+                    }
+                }
+            }
+        }
     }
-    if (tid == 0) st_agent(out.cnt, m);
+    for (int i = tid; i < ne; i += kThreads) {
+        if (sl.ckey[i] >= T0) {
+            const int q = atomicAdd(s_n, 1);
+            if (q < kCapA) {
+                sl.skey[q] = sl.ckey[i];
+                sl.sval[q] = sl.cval[i];
+            }
+        }
+    }
+    __syncthreads();
+    rank_publish(sl.skey, sl.sval, min(*s_n, kCapA), k, sl.rank, out);
 }
 
 // ------------------------------------------------------------- stage B
 // Loads the G sorted chunk lists of a row (one round trip: every slot is
-// requested before any is used) and merges them: the rank of an entry is its
-// index in its own list plus, for every other list, the number of entries
-// greater than it (binary search, all lists in parallel).  Writes the row's
-// top-min(k, total) to okey/oval sorted; returns that count.
+// requested before any is used; every list holds k slots, padded with key 0)
+// and merges them by rank: the rank of a live entry is the number of entries
+// greater than it over all lists (its own list included), each count a
+// branch-free binary search, the searches of one entry advanced in lock-step.
+// Writes the row's top-min(k, total) to okey/oval sorted; returns that count.
 struct MergeLds {
     uint64_t key[kMaxG][kCapA];
     float val[kMaxG][kCapA];
     int cnt[kMaxG];
 };
 
+// Entries of the sorted-descending, zero-padded list L[0, P) greater than
+// `mine` (P a power of two; every read in bounds).
+template <int MG>
+__device__ __forceinline__ void count_greater(const MergeLds &ml, int P, uint64_t mine, int (&pos)[MG]) {
+#pragma unroll
+    for (int h = 0; h < MG; ++h) pos[h] = 0;
+    for (int st = P >> 1; st > 0; st >>= 1) {
+        uint64_t kv[MG];
+#pragma unroll
+        for (int h = 0; h < MG; ++h) kv[h] = ml.key[h][pos[h] + st - 1];
+#pragma unroll
+        for (int h = 0; h < MG; ++h) pos[h] += (kv[h] > mine) ? st : 0;
+    }
+    uint64_t kv[MG];
+#pragma unroll
+    for (int h = 0; h < MG; ++h) kv[h] = ml.key[h][pos[h]];
+#pragma unroll
+    for (int h = 0; h < MG; ++h) pos[h] += (kv[h] > mine) ? 1 : 0;
+}
+
+template <int MG>
+__device__ __forceinline__ void merge_rank(const MergeLds &ml, int G, int P, int need, uint64_t *okey, float *oval) {
+    const int lgP = __builtin_ctz(P);
+    for (int s = threadIdx.x; s < G * P; s += kThreads) {
+        const int g = s >> lgP, i = s & (P - 1);
+        const uint64_t mine = ml.key[g][i];
+        int pos[MG];
+        count_greater<MG>(ml, P, mine, pos);
+        int r = 0;
+#pragma unroll
+        for (int h = 0; h < MG; ++h) r += pos[h];
+        if (mine != 0ull && r < need) {
+            okey[r] = mine;
+            oval[r] = ml.val[g][i];
+        }
+    }
+}
+
 __device__ __forceinline__ int row_merge(const uint64_t *g_key, const float *g_val, const int32_t *g_cnt, int row,
                                          int G, int k, MergeLds &ml, uint64_t *okey, float *oval) {
     const int tid = threadIdx.x;
-    const int slots = G * k;
     const int64_t rb = (int64_t)row * G;
-    // one round trip: every slot of every list is requested before any is used
-    int cn = 0;
-    if (tid < G) cn = ld_agent(&g_cnt[rb + tid]);
-    for (int s0 = 0; s0 < slots; s0 += 4 * kThreads) {
-        uint64_t kk[4];
-        float vv[4];
+    int P = 1;
+    while (P < k) P <<= 1;  // k <= P <= kCapA
+    const int MG = G <= 4 ? 4 : kMaxG;  // lists searched in lock-step (missing ones all zero)
+    if (tid < k) {  // k <= kCapA <= kThreads
+        uint64_t kk[kMaxG];
+        float vv[kMaxG];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            int s = s0 + u * kThreads + tid;
-            if (s < slots) {
-                int g = s / k, i = s - g * k;
-                kk[u] = ld_agent(&g_key[(rb + g) * kCapA + i]);
-                vv[u] = ld_agent(&g_val[(rb + g) * kCapA + i]);
+        for (int g = 0; g < kMaxG; ++g) {
+            if (g < G) {
+                kk[g] = ld_agent(&g_key[(rb + g) * kCapA + tid]);
+                vv[g] = ld_agent(&g_val[(rb + g) * kCapA + tid]);
             }
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            int s = s0 + u * kThreads + tid;
-            if (s < slots) {
-                int g = s / k, i = s - g * k;
-                ml.key[g][i] = kk[u];
-                ml.val[g][i] = vv[u];
+        for (int g = 0; g < kMaxG; ++g) {
+            if (g < G) {
+                ml.key[g][tid] = kk[g];
+                ml.val[g][tid] = vv[g];
             }
         }
     }
-    if (tid < G) ml.cnt[tid] = cn;
+    if (tid < G) ml.cnt[tid] = ld_agent(&g_cnt[rb + tid]);
+    for (int s = tid; s < MG * P; s += kThreads) {  // padding slots and missing lists
+        const int g = s / P, i = s - (s / P) * P;
+        if (g >= G || i >= k) ml.key[g][i] = 0ull;
+    }
     __syncthreads();
     int total = 0;
-    for (int g = 0; g < G; ++g) total += ml.cnt[g];
+#pragma unroll
+    for (int g = 0; g < kMaxG; ++g) total += g < G ? ml.cnt[g] : 0;
     const int need = min(k, total);
-    int half = 1;
-    while (half * 2 <= k) half *= 2;  // largest power of two <= k
-    // rank of entry (g, i) = i + sum over other lists of the entries greater
-    // than it, by branch-free power-of-two searches advanced for every list in
-    // lock-step (their LDS reads are independent and issue together)
-    for (int s = tid; s < slots; s += kThreads) {
-        const int g = s / k, i = s - g * k;
-        const bool live = i < ml.cnt[g];
-        const uint64_t mine = ml.key[g][min(i, kCapA - 1)];
-        int pos[kMaxG], len[kMaxG];
-#pragma unroll
-        for (int h = 0; h < kMaxG; ++h) {
-            pos[h] = 0;
-            len[h] = (h < G && h != g) ? ml.cnt[h] : 0;
-        }
-        for (int st = half; st > 0; st >>= 1) {
-            uint64_t kv[kMaxG];
-#pragma unroll
-            for (int h = 0; h < kMaxG; ++h) kv[h] = ml.key[h][max(min(pos[h] + st, len[h]) - 1, 0)];
-#pragma unroll
-            for (int h = 0; h < kMaxG; ++h) pos[h] += (pos[h] + st <= len[h] && kv[h] > mine) ? st : 0;
-        }
-        int rank = i;
-#pragma unroll
-        for (int h = 0; h < kMaxG; ++h) rank += pos[h];
-        if (live && rank < need) {
-            okey[rank] = mine;
-            oval[rank] = ml.val[g][i];
-        }
-    }
+    if (MG == 4) merge_rank<4>(ml, G, P, need, okey, oval);
+    else merge_rank<kMaxG>(ml, G, P, need, okey, oval);
     __syncthreads();
     return need;
 }

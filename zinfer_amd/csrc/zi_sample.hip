@@ -17,12 +17,9 @@ namespace zi {
 template <bool P>
 struct PenLds {
     PenTable pen;
-    FlagList fl;
 };
 template <>
-struct PenLds<false> {
-    PenTable *pen_ptr() { return nullptr; }
-};
+struct PenLds<false> {};
 
 template <typename T, int NV, bool HAS_PEN>
 struct SampleStageA {
@@ -208,8 +205,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleParams P) {
         SampleStageB b;
     } sm;
     __shared__ uint32_t s_bins[256];
-    __shared__ uint32_t s_tau[kWaves];
-    __shared__ int s_wcnt[kWaves];
+    __shared__ uint32_t s_tau[1];
     __shared__ int s_dig[2];
     __shared__ int s_n, s_flag;
 
@@ -222,19 +218,14 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleParams P) {
     const int c1 = min(a.V, c0 + a.CH);
     const int k = P.k;
 
-    RowPen rp = row_pen(a, row);
     PenTable *pen = nullptr;
-    FlagList *fl = nullptr;
-    if constexpr (HAS_PEN) {
-        pen = &sm.a.p.pen;
-        fl = &sm.a.p.fl;
-    }
+    if constexpr (HAS_PEN) pen = &sm.a.p.pen;
+    PenOwn own;
     ChunkRegs<T, NV> cr;
-    float tmax = chunk_stream<T, NV, HAS_MASK, HAS_PEN>(a, row, c0, c1, cr, pen, fl, rp);
+    chunk_stream<T, NV, HAS_MASK, HAS_PEN>(a, row, c0, c1, cr, pen, &own);
     const int64_t rg = (int64_t)row * G + g;
     ChunkOut out{P.g_key + rg * kCapA, P.g_val + rg * kCapA, P.g_cnt + rg};
-    chunk_select_publish<T, NV, HAS_PEN>(a, rp, cr, tmax, c0, k, sm.a.sel, pen, fl, s_tau, s_wcnt, &s_n, s_bins,
-                                         s_dig, out);
+    chunk_select_publish<T, NV, HAS_PEN>(a, cr, c0, k, sm.a.sel, pen, &own, s_tau, &s_n, s_bins, s_dig, out);
     if (!row_ticket(P.tickets, row, G, &s_flag)) return;
 
     // ---------------- stage B: the last workgroup of this row ----------------
