@@ -133,3 +133,24 @@ def test_config5_full_vocab_reports_unsupported(ctx):
     with pytest.raises(ZiError) as ei:
         ctx.sample_rows(params(temp=1.0, top_k=0, top_p=0.98), L, u, vocab=151936)
     assert ei.value.code == ZI_ERR_UNSUPPORTED
+
+
+@pytest.mark.parametrize("H,win", [(600, 256), (1024, 1000), (3000, 256), (5000, 1000)])
+def test_long_history_rows(ctx, oracle, H, win):
+    """History rows longer than the kernels prefetch (hist_ld > 1024) go
+    through the window compaction first; shorter rows are prefetched whole."""
+    rng = np.random.Generator(np.random.PCG64(H + win))
+    rows, V = 6, 50000
+    x = (rng.standard_t(3, (rows, V)) * 2).astype(np.float32)
+    u = rng.random((rows, 2), dtype=np.float32)
+    hist = rng.integers(0, V, (rows, H), dtype=np.uint32)
+    hist[:, 1::4] = rng.integers(0, 40, (rows, (H + 2) // 4), dtype=np.uint32)[:, : hist[:, 1::4].shape[1]]
+    top = np.argsort(-x, axis=1)[:, :8].astype(np.uint32)  # penalize some of the leaders
+    hist[:, -8:] = top
+    hist_len = np.array([H, H - 1, win // 2, 0, H - win + 3, min(H, 37)], np.int32)
+    pk = dict(temp=0.8, top_k=50, top_p=0.9, min_p=0.05, repeat_penalty=1.3, freq_penalty=0.2,
+              presence_penalty=0.4, penalty_last_n=win)
+    g = gpu_sample(ctx, pk, x, u, hist, hist_len)
+    o = oracle_sample(oracle, pk, x, u, hist, hist_len)
+    errs = compare_sample(g, o, pk, V, f"hist{H}-win{win}")
+    assert not errs, "\n".join(errs[:20])

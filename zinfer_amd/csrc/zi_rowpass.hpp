@@ -208,6 +208,7 @@ __device__ __forceinline__ void pen_mark(PenTable &t, const PenRegs &pr, int c0,
     for (int u = 0; u < kOwnSlots; ++u) {
         const uint32_t id = u < kWinPerThread ? pr.w[u] : pr.e;
         own.id[u] = 0xFFFFFFFFu;
+        own.slot[u] = 0;
         own.x[u] = 0.0f;
         if (id >= (uint32_t)c0 && id < (uint32_t)c1) {
             const uint32_t b = 1u << ((id - c0) & 31);
@@ -522,6 +523,7 @@ struct ChunkOut {
 constexpr int kSortMax = 256;  // candidates ranked without the radix-select path
 constexpr int kCandCap = kThreads * 4;
 constexpr int kStageCap = 32;  // staged vector pairs per wave
+constexpr int kWaveCand = 64;  // candidates per wave region
 
 template <typename T, int NV>
 struct SelectLds {
@@ -529,13 +531,111 @@ struct SelectLds {
     uint32_t uni[kWaves * kMaxR];  // threshold union
     float sx[kWaves][kStageCap * 2 * VEC];  // staged vector pairs
     uint32_t sid[kWaves][kStageCap * 2];
-    uint64_t ckey[kCandCap];  // candidates
+    uint64_t wkey[kWaves][kWaveCand];  // candidates, one region per wave
+    float wval[kWaves][kWaveCand];
+    uint32_t part[kWaves][kSortMax];  // per-region rank counts
+    uint64_t ckey[kCandCap];          // overflow path: penalized keys
     float cval[kCandCap];
     uint64_t skey[kCapA];  // overflow path: the exact top-k, unsorted
     float sval[kCapA];
     uint32_t rank[kSortMax];
     int wcnt[kWaves];
 };
+
+// This wave's candidates: the elements >= tau of its staged vector pairs and
+// (HAS_PEN) of the penalized entries its lanes own, appended to the wave's
+// region by ballot compaction.  Returns the count, which may exceed
+// kWaveCand (entries past it are dropped); no barrier.
+template <typename T, int NV, bool HAS_PEN>
+__device__ __forceinline__ int wave_candidates(const RowSource &a, const ChunkRegs<T, NV> &cr, int c0, float tau,
+                                               SelectLds<T, NV> &sl, const PenTable *t, const PenOwn *own) {
+    constexpr int VEC = VecTraits<T>::VEC;
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int ns = chunk_stage<T, NV>(cr, c0, tau, sl.sx[wid], sl.sid[wid], kStageCap);
+    if (ns > kStageCap) return kWaveCand + 1;
+    uint64_t *wk = sl.wkey[wid];
+    float *wv = sl.wval[wid];
+    int cnt = 0;  // wave-uniform: every lane runs every iteration
+    const int lim = ns * 2 * VEC;
+    for (int q0 = 0; q0 < lim; q0 += 64) {
+        const int q = q0 + lane;
+        const float x = q < lim ? sl.sx[wid][q] : __builtin_nanf("");
+        const bool p = x >= tau;
+        const uint64_t b = ballot(p);
+        const int pos = cnt + lanes_below(b);
+        if (p && pos < kWaveCand) {
+            wk[pos] = ckey(x, sl.sid[wid][q / VEC] + (uint32_t)(q % VEC));
+            wv[pos] = x;
+        }
+        cnt += __popcll(b);
+    }
+    if constexpr (HAS_PEN) {
+#pragma unroll
+        for (int u = 0; u < kOwnSlots; ++u) {
+            const bool mine = own->id[u] != 0xFFFFFFFFu;
+            const float v = mine ? owned_value(a, *t, *own, u) : 0.0f;
+            const bool p = mine && v >= tau;
+            const uint64_t b = ballot(p);
+            const int pos = cnt + lanes_below(b);
+            if (p && pos < kWaveCand) {
+                wk[pos] = ckey(v, own->id[u]);
+                wv[pos] = v;
+            }
+            cnt += __popcll(b);
+        }
+    }
+    return cnt;
+}
+
+// Ranks the n <= kSortMax candidates held in the wave regions (region w has
+// cnt[w] entries, concatenated in wave order) and publishes the first min(n,
+// k) sorted.  Wave w counts, for every candidate, the entries of region w
+// greater than it (broadcast reads); the counts meet after a barrier.  Slots
+// [n, k) get key 0.  Contains a barrier.
+template <typename T, int NV>
+__device__ __forceinline__ void rank_regions(SelectLds<T, NV> &sl, const int (&off)[kWaves + 1], int k,
+                                             ChunkOut out) {
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int n = off[kWaves];
+    const int nb = off[wid + 1] - off[wid];
+    const uint64_t *rk = sl.wkey[wid];
+    for (int i0 = 0; i0 < n; i0 += 64) {
+        const int i = i0 + lane;
+        if (i < n) {
+            int w = 0;
+#pragma unroll
+            for (int q = 1; q < kWaves; ++q) w += (i >= off[q]);
+            int base = 0;
+#pragma unroll
+            for (int q = 1; q < kWaves; ++q) base = (w == q) ? off[q] : base;
+            const uint64_t mine = sl.wkey[w][i - base];
+            uint32_t c = 0;
+            for (int j = 0; j < nb; ++j) c += (uint32_t)(rk[j] > mine);
+            sl.part[wid][i] = c;
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < max(n, k); i += kThreads) {
+        if (i < n) {
+            uint32_t r = 0;
+#pragma unroll
+            for (int q = 0; q < kWaves; ++q) r += sl.part[q][i];
+            if (r < (uint32_t)k) {
+                int w = 0;
+#pragma unroll
+                for (int q = 1; q < kWaves; ++q) w += (i >= off[q]);
+                int base = 0;
+#pragma unroll
+                for (int q = 1; q < kWaves; ++q) base = (w == q) ? off[q] : base;
+                st_agent(&out.key[r], sl.wkey[w][i - base]);
+                st_agent(&out.val[r], sl.wval[w][i - base]);
+            }
+        } else {
+            st_agent(&out.key[i], (uint64_t)0);  // padding: below every real key
+        }
+    }
+    if (tid == 0) st_agent(out.cnt, min(n, k));
+}
 
 // Ranks the n <= kSortMax unique keys by counting, split over the whole
 // workgroup: thread (b, i) counts the keys of block b greater than key i
@@ -582,7 +682,7 @@ __device__ __forceinline__ void chunk_select_publish(const RowSource &a, ChunkRe
     if (tid == 0) *s_n = 0;
     if (tid < kSortMax) sl.rank[tid] = 0u;
     const float tau = chunk_tau(cr.lmax, k, sl.uni, s_tau);  // barriers: *s_n and rank settled
-    const int wc = chunk_stage<T, NV>(cr, c0, tau, sl.sx[wid], sl.sid[wid], kStageCap);
+    const int wc = wave_candidates<T, NV, HAS_PEN>(a, cr, c0, tau, sl, t, own);
     if (lane == 0) sl.wcnt[wid] = wc;
     __syncthreads();
     int off[kWaves + 1];
@@ -590,50 +690,11 @@ __device__ __forceinline__ void chunk_select_publish(const RowSource &a, ChunkRe
     bool overflow = false;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
-        overflow |= sl.wcnt[w] > kStageCap;
-        off[w + 1] = off[w] + min(sl.wcnt[w], kStageCap);
+        overflow |= sl.wcnt[w] > kWaveCand;
+        off[w + 1] = off[w] + min(sl.wcnt[w], kWaveCand);
     }
-    if (!overflow) {  // uniform
-        // expand the staged vectors: one element per thread
-        for (int q = tid; q < off[kWaves] * 2 * VEC; q += kThreads) {
-            const int v = q / (2 * VEC), e = q - v * (2 * VEC);
-            int w = 0;
-#pragma unroll
-            for (int i = 1; i < kWaves; ++i) w += (v >= off[i]);
-            int b = 0;
-#pragma unroll
-            for (int i = 1; i < kWaves; ++i) b = (w == i) ? off[i] : b;
-            const float x = sl.sx[w][(v - b) * 2 * VEC + e];
-            if (x >= tau) {
-                const int pos = atomicAdd(s_n, 1);
-                if (pos < kCandCap) {
-                    sl.ckey[pos] = ckey(x, sl.sid[w][2 * (v - b) + e / VEC] + (uint32_t)(e % VEC));
-                    sl.cval[pos] = x;
-                }
-            }
-        }
-    }
-    if constexpr (HAS_PEN) {
-        if (!overflow) {
-#pragma unroll
-            for (int u = 0; u < kOwnSlots; ++u) {
-                if (own->id[u] != 0xFFFFFFFFu) {
-                    const float v = owned_value(a, *t, *own, u);
-                    if (v >= tau) {
-                        const int pos = atomicAdd(s_n, 1);
-                        if (pos < kCandCap) {
-                            sl.ckey[pos] = ckey(v, own->id[u]);
-                            sl.cval[pos] = v;
-                        }
-                    }
-                }
-            }
-        }
-    }
-    __syncthreads();
-    const int n = *s_n;
-    if (!overflow && n <= kSortMax) {  // uniform: read from LDS after the barrier
-        rank_publish(sl.ckey, sl.cval, n, k, sl.rank, out);
+    if (!overflow && off[kWaves] <= kSortMax) {  // uniform: read from LDS after the barrier
+        rank_regions<T, NV>(sl, off, k, out);
         return;
     }
     // More candidates than the ranking takes (clustered or tied values):
