@@ -90,6 +90,14 @@ __device__ __forceinline__ float wave_serial_chain(float x, float carry, int ste
     return p;
 }
 
+// Orders this wave's LDS writes before its later LDS reads by other lanes
+// (cross-lane exchange through LDS within one wave).
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 __device__ __forceinline__ float readlane_f(float v, int lane) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }

@@ -553,6 +553,7 @@ __device__ __forceinline__ int wave_candidates(const RowSource &a, const ChunkRe
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const int ns = chunk_stage<T, NV>(cr, c0, tau, sl.sx[wid], sl.sid[wid], kStageCap);
     if (ns > kStageCap) return kWaveCand + 1;
+    wave_sync();  // staged by other lanes of this wave
     uint64_t *wk = sl.wkey[wid];
     float *wv = sl.wval[wid];
     int cnt = 0;  // wave-uniform: every lane runs every iteration
