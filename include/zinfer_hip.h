@@ -135,8 +135,13 @@ typedef struct zi_sample_out {
  * `uniforms` [rows][2] (device) stand in for the Zig rng: the first draw is
  * the XTC chance when XTC draws one, else the main draw; ndraws says how many
  * were used so the caller can advance its own generator.
- * Supported: 1 <= top_k <= 256 (or top_k = 0 / top_k > V with V <= 256),
- * penalty window + edits <= 1024 ids. */
+ * Any top_k: lists of up to 256 candidates take one fused pass; top_k = 0
+ * (or >= V) first tries the top-256 prefix with a bounded total and sorts
+ * the rows it cannot settle; 256 < top_k < V always sorts.  For top_k > 256
+ * (with V > 256) cand_ids/cand_vals/probs hold the first min(keep, cand_ld)
+ * candidates (cand_ld >= 1), and the first such call allocates 20 bytes of
+ * sort scratch per (max_rows x max_vocab) entry.  Penalty window + edits <=
+ * 1024 + 128 ids. */
 int32_t zi_sample_rows(zi_ctx *ctx, const zi_params *p, const zi_batch *b,
                        const float *uniforms, const zi_sample_out *out);
 

@@ -118,23 +118,6 @@ def test_config_full_size_parity(ctx, oracle, cfg):
         assert not errs, "\n".join(errs)
 
 
-def test_config5_full_vocab_reports_unsupported(ctx):
-    """top_k = 0 over V = 151936 (config 5) needs the whole-vocabulary nucleus
-    path, which this build does not implement yet: the call must fail loudly,
-    not fall back."""
-    import torch
-    from zinfer_amd._lib import ZI_ERR_UNSUPPORTED, ZiError
-    from zinfer_amd.api import params
-    from paritylib import to_device
-
-    x = np.zeros((2, 151936), np.float32)
-    L = to_device(x, bf16=True)
-    u = torch.zeros((2, 2), device="cuda")
-    with pytest.raises(ZiError) as ei:
-        ctx.sample_rows(params(temp=1.0, top_k=0, top_p=0.98), L, u, vocab=151936)
-    assert ei.value.code == ZI_ERR_UNSUPPORTED
-
-
 @pytest.mark.parametrize("H,win", [(600, 256), (1024, 1000), (3000, 256), (5000, 1000)])
 def test_long_history_rows(ctx, oracle, H, win):
     """History rows longer than the kernels prefetch (hist_ld > 1024) go

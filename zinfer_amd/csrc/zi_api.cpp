@@ -119,8 +119,8 @@ extern "C" void zi_destroy(zi_ctx *c) {
     if (!c) return;
     hipSetDevice(c->device);
     if (c->own_stream) hipStreamSynchronize(c->own_stream);
-    void *ptrs[] = {c->g_key, c->g_val,  c->g_cnt,  c->tickets, c->g_stat, c->g_cls,
-                    c->g_raw, c->g_top2, c->g_tail, c->win_ids, c->win_len};
+    void *ptrs[] = {c->g_key,  c->g_val,   c->g_cnt,   c->tickets, c->g_stat,  c->g_cls,   c->g_raw,
+                    c->g_top2, c->g_tail,  c->win_ids, c->win_len, c->ex_sort, c->nuc_flag};
     for (void *p : ptrs)
         if (p) hipFree(p);
     if (c->own_stream) hipStreamDestroy(c->own_stream);
@@ -242,6 +242,93 @@ static int32_t run_argmax(zi_ctx *c, const zi::RowSource &src, const zi_batch *b
     return ZI_OK;
 }
 
+// Candidate lists longer than kMaxTopK.  k = V: nucleus_kernel settles the
+// rows whose keep its 256-entry prefix fixes and flags the rest for
+// exact_kernel; 256 < k < V: exact_kernel on every row.  The sort scratch
+// (20 bytes per row entry) is allocated on first use.
+static int32_t run_whole_order(zi_ctx *c, const zi_params *p, const zi_batch *b, const zi::RowSource &src,
+                               const zi::Plan &pl, uint32_t k, const float *uniforms, const zi_sample_out *out) {
+    if ((out->cand_ids || out->cand_vals || out->probs) && out->cand_ld < 1)
+        return zi_fail(ZI_ERR_INVALID, "zi_sample_rows: cand_ld=%d < 1", out->cand_ld);
+    if (!c->ex_sort) {
+        const int64_t ld = ((int64_t)c->max_vocab + 7) / 8 * 8;
+        const size_t bytes = 5 * (size_t)c->max_rows * (size_t)ld * sizeof(uint32_t);
+        hipError_t e = hipMalloc((void **)&c->ex_sort, bytes);
+        if (e == hipSuccess) e = hipMalloc((void **)&c->nuc_flag, (size_t)c->max_rows * sizeof(int32_t));
+        if (e != hipSuccess) {
+            if (c->ex_sort) hipFree(c->ex_sort);
+            c->ex_sort = nullptr;
+            c->nuc_flag = nullptr;
+            return zi_fail(ZI_ERR_OOM, "zi_sample_rows: sort scratch %zu bytes: %s", bytes, hipGetErrorString(e));
+        }
+        c->ex_ld = ld;
+    }
+    const uint32_t V = (uint32_t)b->vocab;
+    const bool whole = k >= V;
+    if (whole) {
+        zi::SampleParams P;
+        std::memset(&P, 0, sizeof P);
+        P.src = src;
+        P.k = zi::kMaxTopK;  // prefix length
+        P.temp = p->temp;
+        P.top_p = p->top_p;
+        P.min_p = p->min_p;
+        P.xtc_p = p->xtc_probability;
+        P.xtc_thr = p->xtc_threshold;
+        P.xtc_min_keep = (int)(p->xtc_min_keep > 0x7FFFFFFFu ? 0x7FFFFFFFu : p->xtc_min_keep);
+        P.uniforms = uniforms;
+        P.tok = out->tok;
+        P.margin = out->margin;
+        P.ndraws = out->ndraws;
+        P.keep = out->keep;
+        P.cand_ids = out->cand_ids;
+        P.cand_vals = out->cand_vals;
+        P.probs = out->probs;
+        P.cand_ld = out->cand_ld;
+        P.g_key = c->g_key;
+        P.g_val = c->g_val;
+        P.g_cnt = c->g_cnt;
+        P.tickets = c->tickets;
+        P.n_all = (int)V;
+        P.g_stat = c->g_stat;
+        P.nuc_flag = c->nuc_flag;
+        hipError_t e = zi::launch_nucleus(P, b->dtype, pl.nv, b->rows, c->stream);
+        if (e != hipSuccess) return zi_hip_fail(e, "nucleus kernel launch");
+    }
+    zi::ExactParams X;
+    std::memset(&X, 0, sizeof X);
+    X.src = src;
+    X.n = (int)k;
+    X.temp = p->temp;
+    X.top_p = p->top_p;
+    X.min_p = p->min_p;
+    X.xtc_p = p->xtc_probability;
+    X.xtc_thr = p->xtc_threshold;
+    X.xtc_min_keep = (int)(p->xtc_min_keep > 0x7FFFFFFFu ? 0x7FFFFFFFu : p->xtc_min_keep);
+    X.uniforms = uniforms;
+    X.tok = out->tok;
+    X.margin = out->margin;
+    X.ndraws = out->ndraws;
+    X.keep = out->keep;
+    X.cand_ids = out->cand_ids;
+    X.cand_vals = out->cand_vals;
+    X.probs = out->probs;
+    X.cand_ld = out->cand_ld;
+    X.flags = whole ? c->nuc_flag : nullptr;
+    X.g_stat = whole ? c->g_stat : nullptr;
+    X.n_all = (int)V;
+    const size_t plane = (size_t)c->max_rows * (size_t)c->ex_ld;
+    X.keys = c->ex_sort;
+    X.key0 = c->ex_sort + plane;
+    X.id0 = c->ex_sort + 2 * plane;
+    X.key1 = c->ex_sort + 3 * plane;
+    X.id1 = c->ex_sort + 4 * plane;
+    X.ldk = c->ex_ld;
+    hipError_t e = zi::launch_exact(X, b->dtype, b->rows, c->stream);
+    if (e != hipSuccess) return zi_hip_fail(e, "exact kernel launch");
+    return ZI_OK;
+}
+
 extern "C" int32_t zi_sample_rows(zi_ctx *c, const zi_params *p, const zi_batch *b, const float *uniforms,
                                   const zi_sample_out *out) {
     int32_t rc = check_batch(c, b, "zi_sample_rows");
@@ -268,9 +355,7 @@ extern "C" int32_t zi_sample_rows(zi_ctx *c, const zi_params *p, const zi_batch 
     if (!uniforms) return zi_fail(ZI_ERR_INVALID, "zi_sample_rows: uniforms is NULL");
     const uint32_t V = (uint32_t)b->vocab;
     const uint32_t k = (p->top_k == 0 || p->top_k > V) ? V : p->top_k;  // src/sampler.zig:197
-    if (k > (uint32_t)zi::kMaxTopK)
-        return zi_fail(ZI_ERR_UNSUPPORTED, "zi_sample_rows: top-k size %u > %d is not implemented", k,
-                       zi::kMaxTopK);
+    if (k > (uint32_t)zi::kMaxTopK) return run_whole_order(c, p, b, src, pl, k, uniforms, out);
     if ((out->cand_ids || out->cand_vals || out->probs) && out->cand_ld < (int32_t)k)
         return zi_fail(ZI_ERR_INVALID, "zi_sample_rows: cand_ld=%d < k=%u", out->cand_ld, k);
 

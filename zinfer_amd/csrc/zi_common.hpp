@@ -98,6 +98,20 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) v += __shfl_xor(v, m);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max_f(float v) {
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) v = fmaxf(v, __shfl_xor(v, m));
+    return v;
+}
+
 __device__ __forceinline__ float readlane_f(float v, int lane) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
@@ -159,6 +173,64 @@ __device__ __forceinline__ uint32_t sort_from_u32(uint32_t x) {
 }
 
 __device__ __forceinline__ uint32_t wave_sort_desc_u32(uint32_t x) { return sort_from_u32<2>(x); }
+
+// Sequential f32 sum over s[i0, i1), added in index order onto `acc`, by the
+// one calling lane: the reference's loop order exactly, at one dependent add
+// per term (4 terms per LDS read).
+__device__ __forceinline__ float lane_sum(const float *s, int i0, int i1, float acc) {
+    int i = i0;
+    for (; i < i1 && (i & 3); ++i) acc = acc + s[i];
+    for (; i + 4 <= i1; i += 4) {
+        const float4 v = *reinterpret_cast<const float4 *>(s + i);
+        acc = acc + v.x;
+        acc = acc + v.y;
+        acc = acc + v.z;
+        acc = acc + v.w;
+    }
+    for (; i < i1; ++i) acc = acc + s[i];
+    return acc;
+}
+
+// 1 + the first i < end whose prefix sum fl(...fl(0 + s_0) ... + s_i) is
+// >= thr (`none` if there is none).  The terms are >= 0, so the rounded
+// prefixes never decrease and a block of four can be tested by its last.
+__device__ __forceinline__ int first_reach(const float *s, int end, float thr, int none) {
+    float acc = 0.0f;
+    int i = 0;
+    for (; i + 4 <= end; i += 4) {
+        const float4 v = *reinterpret_cast<const float4 *>(s + i);
+        const float p0 = acc + v.x, p1 = p0 + v.y, p2 = p1 + v.z, p3 = p2 + v.w;
+        if (p3 >= thr) return i + (p0 >= thr ? 1 : p1 >= thr ? 2 : p2 >= thr ? 3 : 4);
+        acc = p3;
+    }
+    for (; i < end; ++i) {
+        acc = acc + s[i];
+        if (acc >= thr) return i + 1;
+    }
+    return none;
+}
+
+// The first i in [start, end) at which r = fl(r - s_i), applied in order
+// from i = start, is <= 0, else end - 1 (the draw's fallback).  The terms are
+// >= 0, so r never increases and a block of four is tested by its last.
+__device__ __forceinline__ int first_drop(const float *s, int start, int end, float r) {
+    int i = start;
+    for (; i < end && (i & 3); ++i) {
+        r = r - s[i];
+        if (r <= 0.0f) return i;
+    }
+    for (; i + 4 <= end; i += 4) {
+        const float4 v = *reinterpret_cast<const float4 *>(s + i);
+        const float d0 = r - v.x, d1 = d0 - v.y, d2 = d1 - v.z, d3 = d2 - v.w;
+        if (d3 <= 0.0f) return i + (d0 <= 0.0f ? 0 : d1 <= 0.0f ? 1 : d2 <= 0.0f ? 2 : 3);
+        r = d3;
+    }
+    for (; i < end; ++i) {
+        r = r - s[i];
+        if (r <= 0.0f) return i;
+    }
+    return end - 1;
+}
 
 template <typename T>
 struct VecTraits;

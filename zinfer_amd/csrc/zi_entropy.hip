@@ -26,20 +26,6 @@ struct EntStageB {
     float oval[kThreads];
 };
 
-constexpr float kLog2e = 1.4426950408889634f;
-
-__device__ __forceinline__ double wave_sum_d(double v) {
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) v += __shfl_xor(v, m);
-    return v;
-}
-
-__device__ __forceinline__ float wave_max_f(float v) {
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) v = fmaxf(v, __shfl_xor(v, m));
-    return v;
-}
-
 // Per-thread running (ref, S, U), updated per vector as its load lands.
 struct EntHook {
     float *ref, *S, *U;

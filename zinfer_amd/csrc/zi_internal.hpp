@@ -23,6 +23,10 @@ struct zi_ctx {
     float *g_tail = nullptr;
     uint32_t *win_ids = nullptr;  // [max_rows][kMaxWinHost] compacted penalty windows
     int32_t *win_len = nullptr;   // [max_rows]
+    // whole-order sampling (top_k > 256), allocated on first use
+    uint32_t *ex_sort = nullptr;  // 5 x [max_rows][ex_ld] keys in id order, sort keys / ids
+    int64_t ex_ld = 0;
+    int32_t *nuc_flag = nullptr;  // [max_rows]
 };
 
 int32_t zi_fail(int32_t code, const char *fmt, ...);

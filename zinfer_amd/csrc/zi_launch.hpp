@@ -58,6 +58,33 @@ struct SampleParams {
     float *g_val;
     int32_t *g_cnt;    // [rows][G]
     int32_t *tickets;  // [rows], zero between launches
+    // whole-vocabulary rows (nucleus_kernel only)
+    int n_all;          // the reference's candidate count (V)
+    double *g_stat;     // [rows][G][3]: chunk max, sum exp(x - max)
+    int32_t *nuc_flag;  // [rows] out: 1 = keep not fixed by the prefix, run exact_kernel
+};
+
+// Exact whole-order sampling of one row per workgroup (top_k = 0 rows the
+// prefix could not settle, and 256 < top_k < V).
+struct ExactParams {
+    RowSource src;
+    int n;  // candidate count: min(top_k or V, V)
+    float temp, top_p, min_p, xtc_p, xtc_thr;
+    int xtc_min_keep;
+    const float *uniforms;
+    uint32_t *tok;
+    float *margin;
+    int32_t *ndraws;
+    int32_t *keep;
+    uint32_t *cand_ids;
+    float *cand_vals;
+    float *probs;
+    int cand_ld;
+    const int32_t *flags;  // [rows]: row r runs iff flags[r] != 0; NULL: every row
+    const double *g_stat;  // [rows][G][3] chunk (max, sum exp(x - max)) of the prefix pass, or NULL
+    int n_all;             // V when g_stat bounds the whole-vocabulary total
+    uint32_t *keys, *key0, *id0, *key1, *id1;  // scratch [rows][ldk]: keys in id order, sort buffers
+    int64_t ldk;                               // >= V rounded up to 8
 };
 
 struct ArgmaxParams {
@@ -100,6 +127,8 @@ struct MaskParams {
 };
 
 hipError_t launch_sample(const SampleParams &P, int dtype, int nv, int rows, hipStream_t st);
+hipError_t launch_nucleus(const SampleParams &P, int dtype, int nv, int rows, hipStream_t st);
+hipError_t launch_exact(const ExactParams &P, int dtype, int rows, hipStream_t st);
 hipError_t launch_argmax(const ArgmaxParams &P, int dtype, int nv, int rows, hipStream_t st);
 hipError_t launch_entropy(const EntropyParams &P, int dtype, int nv, int rows, hipStream_t st);
 hipError_t launch_mask(const MaskParams &P, hipStream_t st);

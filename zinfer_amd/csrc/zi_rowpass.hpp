@@ -76,7 +76,8 @@ __device__ __forceinline__ uint32_t hash_slot(uint32_t id, int hs_log2) {
     return (id * 2654435761u) >> (32 - hs_log2);
 }
 
-__device__ __forceinline__ int pen_insert(PenTable &t, uint32_t id, int hs_log2) {
+template <class Table>  // PenTable or any table with the same key array
+__device__ __forceinline__ int pen_insert(Table &t, uint32_t id, int hs_log2) {
     uint32_t h = hash_slot(id, hs_log2);
     const uint32_t m = (1u << hs_log2) - 1;
     for (;;) {
@@ -669,6 +670,30 @@ __device__ __forceinline__ void rank_publish(const uint64_t *keys, const float *
     if (tid == 0) st_agent(out.cnt, min(n, k));
 }
 
+// Ranks n <= kRankMax unique keys by counting (each key's rank is the number
+// of keys greater than it; counting stops at k) and publishes the first
+// min(n, k) sorted; slots [n, k) get key 0.  No barrier.
+constexpr int kRankMax = 1024;
+__device__ __forceinline__ void rank_count(const uint64_t *keys, const float *vals, int n, int k, ChunkOut out) {
+    const int tid = threadIdx.x;
+    for (int i = tid; i < n; i += kThreads) {
+        const uint64_t mine = keys[i];
+        uint32_t c = 0;
+        int j = 0;
+        for (; j + 8 <= n && c < (uint32_t)k; j += 8) {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) c += (uint32_t)(keys[j + q] > mine);
+        }
+        for (; j < n; ++j) c += (uint32_t)(keys[j] > mine);
+        if (c < (uint32_t)k) {
+            st_agent(&out.key[c], mine);
+            st_agent(&out.val[c], vals[i]);
+        }
+    }
+    for (int i = n + tid; i < k; i += kThreads) st_agent(&out.key[i], (uint64_t)0);  // padding
+    if (tid == 0) st_agent(out.cnt, min(n, k));
+}
+
 // Stage A after chunk_stream: find the chunk's exact top-min(k, selectable)
 // sorted by (value desc, id asc), publish it to `out` (agent-scope stores).
 // LDS: `sl` (SelectLds), `t` when HAS_PEN (with the owners in `own`), small
@@ -698,8 +723,51 @@ __device__ __forceinline__ void chunk_select_publish(const RowSource &a, ChunkRe
         rank_regions<T, NV>(sl, off, k, out);
         return;
     }
-    // More candidates than the ranking takes (clustered or tied values):
-    // exact radix select over registers + penalized entries, then rank the top-k.
+    // More candidates than the wave regions take: every entry >= tau (the
+    // top-k are among them) is gathered and ranked by counting.
+    if (tid == 0) *s_n = 0;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        if (cr.m4[j] >= tau) {  // NaN (empty vector) fails
+            const int e0 = c0 + (j * kThreads + tid) * VEC;
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) {
+                const float x = cr.x[j * VEC + e];
+                if (x >= tau) {
+                    const int q = atomicAdd(s_n, 1);
+                    if (q < kCandCap) {
+                        sl.ckey[q] = ckey(x, (uint32_t)(e0 + e));
+                        sl.cval[q] = x;
+                    }
+                }
+            }
+        }
+    }
+    if constexpr (HAS_PEN) {
+#pragma unroll
+        for (int u = 0; u < kOwnSlots; ++u) {
+            if (own->id[u] != 0xFFFFFFFFu) {
+                const float v = owned_value(a, *t, *own, u);
+                if (v >= tau) {
+                    const int q = atomicAdd(s_n, 1);
+                    if (q < kCandCap) {
+                        sl.ckey[q] = ckey(v, own->id[u]);
+                        sl.cval[q] = v;
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();
+    const int nc = *s_n;
+    if (nc <= kRankMax) {  // uniform
+        rank_count(sl.ckey, sl.cval, nc, k, out);
+        return;
+    }
+    // Still too many (ties, flat rows): exact radix select over registers +
+    // penalized entries, then rank the top-k.
+    __syncthreads();  // every thread has read *s_n before it is reset
     int ne = 0;
     if constexpr (HAS_PEN) {
         if (tid == 0) *s_n = 0;

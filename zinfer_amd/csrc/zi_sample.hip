@@ -1,5 +1,6 @@
 // zi_sample.hip -- batched Sampler.sampleWithMargin (src/sampler.zig:190-276)
-// for top_k in [1, 256].
+// for top_k in [1, 256], and the first pass of whole-vocabulary rows (top_k =
+// 0 or >= V, src/sampler.zig:197-201).
 //
 // One launch covers the batch: grid = rows x G workgroups.  Stage A (every
 // workgroup) streams its chunk of the row from HBM once with 16-byte loads,
@@ -37,68 +38,60 @@ struct SampleStageB {
     TailLds tl;
 };
 
-// Sequential f32 sum over s[i0, i1), added in index order onto `acc`, by the
-// one calling lane: the reference's loop order exactly, at one dependent add
-// per term (4 terms per LDS read).
-__device__ __forceinline__ float lane_sum(const float *s, int i0, int i1, float acc) {
-    int i = i0;
-    for (; i < i1 && (i & 3); ++i) acc = acc + s[i];
-    for (; i + 4 <= i1; i += 4) {
-        const float4 v = *reinterpret_cast<const float4 *>(s + i);
-        acc = acc + v.x;
-        acc = acc + v.y;
-        acc = acc + v.z;
-        acc = acc + v.w;
+// Whole-vocabulary rows (k = V): the reference's top-p total runs over all V
+// terms in sorted order (src/sampler.zig:217-218), but only the row's first n
+// candidates are at hand.  The stream bounds that total: the chunks' sums of
+// exp(x - max) give T within a relative 1e-4 (hardware exp2 with f32 partial
+// sums, well inside that), and a sequential f32 sum of V nonnegative terms is
+// within gamma_{V-1} = (V-1)u / (1 - (V-1)u) of the exact sum (u = 2^-24).  So
+// the reference's threshold fl(top_p * total) lies in [fl(top_p * lo),
+// fl(top_p * hi)] and its keep in [kp_lo, kp_hi].  keep is settled when
+// min-p cuts before kp_lo, or when kp_lo == kp_hi within the prefix; then the
+// rest of the tail only reads the prefix.  Lane 0 only; returns false when
+// the row needs the exact whole-order pass.
+__device__ __forceinline__ bool nucleus_keep(const SampleParams &P, int row, const float *e, int n, int live,
+                                             int first_low, float mx, int &keep) {
+    int kp_lo = n + 1, kp_hi = n + 1;  // n + 1: past the prefix
+    if (P.top_p < 1.0f) {
+        if (!__builtin_isfinite(mx)) return false;
+        const int G = P.src.G;
+        const double *gs = P.g_stat + (int64_t)row * G * 3;
+        double Mr = -INFINITY;
+        for (int g = 0; g < G; ++g) Mr = fmax(Mr, ld_agent(&gs[g * 3]));
+        double Z = 0.0;
+        for (int g = 0; g < G; ++g) {
+            const double m = ld_agent(&gs[g * 3]);
+            if (m != -INFINITY) Z += ld_agent(&gs[g * 3 + 1]) * exp(m - Mr);
+        }
+        const double T = Z * exp(Mr - (double)mx);
+        if (!(T >= 0.5 && T < 1e30)) return false;  // the term of the maximum alone is 1
+        const double nu = (double)(P.n_all - 1) * 0x1p-24;
+        const double gam = nu / (1.0 - nu) + 1e-4;
+        const double dlo = T * (1.0 - gam), dhi = T * (1.0 + gam);
+        float lo = (float)dlo, hi = (float)dhi;
+        if ((double)lo > dlo) lo = __uint_as_float(__float_as_uint(lo) - 1u);  // round down (lo > 0)
+        if ((double)hi < dhi) hi = __uint_as_float(__float_as_uint(hi) + 1u);  // round up
+        kp_lo = first_reach(e, live, P.top_p * lo, n + 1);
+        kp_hi = first_reach(e, live, P.top_p * hi, n + 1);
     }
-    for (; i < i1; ++i) acc = acc + s[i];
-    return acc;
-}
-
-// 1 + the first i < end whose prefix sum fl(...fl(0 + s_0) ... + s_i) is
-// >= thr (`none` if there is none).  The terms are >= 0, so the rounded
-// prefixes never decrease and a block of four can be tested by its last.
-__device__ __forceinline__ int first_reach(const float *s, int end, float thr, int none) {
-    float acc = 0.0f;
-    int i = 0;
-    for (; i + 4 <= end; i += 4) {
-        const float4 v = *reinterpret_cast<const float4 *>(s + i);
-        const float p0 = acc + v.x, p1 = p0 + v.y, p2 = p1 + v.z, p3 = p2 + v.w;
-        if (p3 >= thr) return i + (p0 >= thr ? 1 : p1 >= thr ? 2 : p2 >= thr ? 3 : 4);
-        acc = p3;
+    if (first_low < n && first_low < kp_lo) {  // min-p cuts before any possible keep (:229-234)
+        keep = first_low > 1 ? first_low : 1;
+        return true;
     }
-    for (; i < end; ++i) {
-        acc = acc + s[i];
-        if (acc >= thr) return i + 1;
+    if (kp_lo == kp_hi && kp_lo <= n) {  // top-p keep pinned, min-p does not cut before it
+        keep = kp_lo;
+        return true;
     }
-    return none;
-}
-
-// The first i in [start, end) at which r = fl(r - s_i), applied in order
-// from i = start, is <= 0, else end - 1 (the draw's fallback).  The terms are
-// >= 0, so r never increases and a block of four is tested by its last.
-__device__ __forceinline__ int first_drop(const float *s, int start, int end, float r) {
-    int i = start;
-    for (; i < end && (i & 3); ++i) {
-        r = r - s[i];
-        if (r <= 0.0f) return i;
-    }
-    for (; i + 4 <= end; i += 4) {
-        const float4 v = *reinterpret_cast<const float4 *>(s + i);
-        const float d0 = r - v.x, d1 = d0 - v.y, d2 = d1 - v.z, d3 = d2 - v.w;
-        if (d3 <= 0.0f) return i + (d0 <= 0.0f ? 0 : d1 <= 0.0f ? 1 : d2 <= 0.0f ? 2 : 3);
-        r = d3;
-    }
-    for (; i < end; ++i) {
-        r = r - s[i];
-        if (r <= 0.0f) return i;
-    }
-    return end - 1;
+    return false;
 }
 
 // The reference tail (src/sampler.zig:211-275) on the row's n sorted
 // candidates, one wave with all 64 lanes active.  The lanes compute the
 // exponentials; the sequential sums (top-p, temperature total, draw) run on
-// lane 0 from LDS, in the reference's order.
+// lane 0 from LDS, in the reference's order.  NUC: the n candidates are the
+// prefix of a whole-vocabulary row (nucleus_keep); an unsettled row only sets
+// its flag, and the candidate outputs cover the kept entries.
+template <bool NUC>
 __device__ __forceinline__ void sample_tail(const SampleParams &P, int row, const uint64_t *okey, const float *oval,
                                             int n, TailLds &tl, float u0, float u1) {
     const int lane = threadIdx.x;
@@ -156,15 +149,25 @@ __device__ __forceinline__ void sample_tail(const SampleParams &P, int row, cons
     wave_sync();  // tl.e / tl.w complete before lane 0 reads them
     int keep0 = n;
     float total0 = 0.0f;
+    int settled0 = 1;
     if (lane == 0) {
         int keep = n;
-        if (P.top_p < 1.0f) {  // :215-226
-            const float thr = P.top_p * lane_sum(tl.e, 0, live, 0.0f);
-            keep = first_reach(tl.e, live, thr, n);
+        if constexpr (NUC) {
+            settled0 = nucleus_keep(P, row, tl.e, n, live, first_low, mx, keep) ? 1 : 0;
+        } else {
+            if (P.top_p < 1.0f) {  // :215-226
+                const float thr = P.top_p * lane_sum(tl.e, 0, live, 0.0f);
+                keep = first_reach(tl.e, live, thr, n);
+            }
+            if (first_low < keep) keep = first_low > 1 ? first_low : 1;
         }
-        if (first_low < keep) keep = first_low > 1 ? first_low : 1;
         keep0 = keep;
-        total0 = lane_sum(tl.w, 0, keep, 0.0f);  // :236-242
+        if (settled0) total0 = lane_sum(tl.w, 0, keep, 0.0f);  // :236-242
+    }
+    if constexpr (NUC) {
+        const int settled = __builtin_amdgcn_readlane(settled0, 0);
+        if (lane == 0) P.nuc_flag[row] = settled ? 0 : 1;
+        if (!settled) return;
     }
     const int keep = __builtin_amdgcn_readlane(keep0, 0);
     float total = readlane_f(total0, 0);
@@ -207,10 +210,11 @@ __device__ __forceinline__ void sample_tail(const SampleParams &P, int row, cons
         if (P.keep) P.keep[row] = keep;
     }
     if (P.cand_ids) {
+        const int n_out = NUC ? min(keep, P.cand_ld) : n;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             int i = lane + 64 * c;
-            if (i < n) {
+            if (i < n_out) {
                 int64_t o = (int64_t)row * P.cand_ld + i;
                 P.cand_ids[o] = cid[c];
                 if (P.cand_vals) P.cand_vals[o] = cv[c];
@@ -268,39 +272,145 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleParams P) {
         }
         return;
     }
-    sample_tail(P, row, sm.b.okey, sm.b.oval, n, sm.b.tl, u0, u1);
+    sample_tail<false>(P, row, sm.b.okey, sm.b.oval, n, sm.b.tl, u0, u1);
 }
 
-template <typename T, int NV, bool M, bool PN>
+// Per-thread running (ref, S) with S = sum exp(x - ref) over the thread's
+// elements, updated per vector as its load lands; ref moves up only when an
+// element exceeds it by 64, so S cannot overflow.  -inf, NaN (diverted or
+// past the chunk) contribute 0.
+struct SumHook {
+    float *ref, *S;
+    template <int VEC>
+    __device__ void operator()(int, const float (&v)[VEC], float m4) const {
+        if (m4 > *ref + 64.0f) {  // also the first finite value (ref = -inf)
+            if (*ref != -INFINITY) *S = *S * __builtin_amdgcn_exp2f((*ref - m4) * kLog2e);
+            *ref = m4;
+        }
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) *S = *S + __builtin_amdgcn_exp2f(fmaxf(v[e] - *ref, -200.0f) * kLog2e);
+    }
+};
+
+// First pass of whole-vocabulary rows: sample_kernel's stream and selection
+// with a k-entry prefix (k = kMaxTopK), plus each chunk's (max, sum exp(x -
+// max)) for the bound on the reference's total.  Rows whose keep the prefix
+// settles are finished here; the others get nuc_flag = 1 for exact_kernel.
+template <typename T, int NV, bool HAS_MASK, bool HAS_PEN>
+__global__ __launch_bounds__(kThreads) void nucleus_kernel(SampleParams P) {
+    __shared__ union {
+        SampleStageA<T, NV, HAS_PEN> a;
+        SampleStageB b;
+    } sm;
+    __shared__ uint32_t s_bins[256];
+    __shared__ uint32_t s_tau[1];
+    __shared__ int s_dig[2];
+    __shared__ int s_n, s_flag;
+    __shared__ float s_wmax[kWaves];
+    __shared__ double s_ws[kWaves];
+
+    const RowSource &a = P.src;
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int G = a.G;
+    const int row = blockIdx.x / G;
+    const int g = blockIdx.x - row * G;
+    const int c0 = g * a.CH;
+    const int c1 = min(a.V, c0 + a.CH);
+    const int k = P.k;
+
+    PenTable *pen = nullptr;
+    if constexpr (HAS_PEN) pen = &sm.a.p.pen;
+    PenOwn own;
+    ChunkRegs<T, NV> cr;
+    float ref = -INFINITY, S = 0.0f;
+    chunk_stream<T, NV, HAS_MASK, HAS_PEN, SumHook>(a, row, c0, c1, cr, pen, &own, SumHook{&ref, &S});
+    int ur = 2 * row;
+    asm volatile("" : "+v"(ur));
+    const float u0 = P.uniforms[ur], u1 = P.uniforms[ur + 1];
+    const int64_t rg = (int64_t)row * G + g;
+    ChunkOut out{P.g_key + rg * kCapA, P.g_val + rg * kCapA, P.g_cnt + rg};
+    chunk_select_publish<T, NV, HAS_PEN>(a, cr, c0, k, sm.a.sel, pen, &own, s_tau, &s_n, s_bins, s_dig, out);
+    if constexpr (HAS_PEN) {  // the penalized entries this thread owns (hash settled by the barriers above)
+#pragma unroll
+        for (int u = 0; u < kOwnSlots; ++u) {
+            if (own.id[u] != 0xFFFFFFFFu) {
+                const float v = owned_value(a, *pen, own, u);
+                if (v > ref) {
+                    S = S * __builtin_amdgcn_exp2f((ref - v) * kLog2e) + 1.0f;
+                    ref = v;
+                } else if (v > -INFINITY) {
+                    S = S + __builtin_amdgcn_exp2f(fmaxf(v - ref, -200.0f) * kLog2e);
+                }
+            }
+        }
+    }
+    const float wm = wave_max_f(ref);
+    if (lane == 0) s_wmax[wid] = wm;
+    __syncthreads();
+    float M = s_wmax[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) M = fmaxf(M, s_wmax[w]);
+    double ds = (ref != -INFINITY && M != -INFINITY) ? (double)S * exp((double)ref - (double)M) : 0.0;
+    ds = wave_sum_d(ds);
+    if (lane == 0) s_ws[wid] = ds;
+    __syncthreads();
+    if (tid == 0) {
+        double ts = 0.0;
+        for (int w = 0; w < kWaves; ++w) ts += s_ws[w];
+        st_agent(&P.g_stat[rg * 3], (double)M);
+        st_agent(&P.g_stat[rg * 3 + 1], ts);
+    }
+    if (!row_ticket(P.tickets, row, G, &s_flag)) return;
+
+    const int n = row_merge(P.g_key, P.g_val, P.g_cnt, row, G, k, sm.b.ml, sm.b.okey, sm.b.oval);
+    if (tid >= 64) return;
+    if (n == 0) {  // no selectable logit: let the exact pass apply the reference literally
+        if (tid == 0) P.nuc_flag[row] = 1;
+        return;
+    }
+    sample_tail<true>(P, row, sm.b.okey, sm.b.oval, n, sm.b.tl, u0, u1);
+}
+
+template <bool NUC, typename T, int NV, bool M, bool PN>
 static hipError_t launch_sample_t(const SampleParams &P, int rows, hipStream_t st) {
     dim3 grid(rows * P.src.G), block(kThreads);
-    hipLaunchKernelGGL((sample_kernel<T, NV, M, PN>), grid, block, 0, st, P);
+    if constexpr (NUC) hipLaunchKernelGGL((nucleus_kernel<T, NV, M, PN>), grid, block, 0, st, P);
+    else hipLaunchKernelGGL((sample_kernel<T, NV, M, PN>), grid, block, 0, st, P);
     return hipGetLastError();
 }
 
-template <typename T, int NV>
+template <bool NUC, typename T, int NV>
 static hipError_t launch_sample_nv(const SampleParams &P, int rows, hipStream_t st) {
     const bool m = P.src.mask != nullptr;
     const bool p = (P.src.hist != nullptr) || (P.src.edit_ids != nullptr);
-    if (m && p) return launch_sample_t<T, NV, true, true>(P, rows, st);
-    if (m) return launch_sample_t<T, NV, true, false>(P, rows, st);
-    if (p) return launch_sample_t<T, NV, false, true>(P, rows, st);
-    return launch_sample_t<T, NV, false, false>(P, rows, st);
+    if (m && p) return launch_sample_t<NUC, T, NV, true, true>(P, rows, st);
+    if (m) return launch_sample_t<NUC, T, NV, true, false>(P, rows, st);
+    if (p) return launch_sample_t<NUC, T, NV, false, true>(P, rows, st);
+    return launch_sample_t<NUC, T, NV, false, false>(P, rows, st);
 }
 
-hipError_t launch_sample(const SampleParams &P, int dtype, int nv, int rows, hipStream_t st) {
+template <bool NUC>
+static hipError_t launch_dispatch(const SampleParams &P, int dtype, int nv, int rows, hipStream_t st) {
     if (dtype == 0) {
         switch (nv) {
-            case 4: return launch_sample_nv<float, 4>(P, rows, st);
-            case 8: return launch_sample_nv<float, 8>(P, rows, st);
-            default: return launch_sample_nv<float, 16>(P, rows, st);
+            case 4: return launch_sample_nv<NUC, float, 4>(P, rows, st);
+            case 8: return launch_sample_nv<NUC, float, 8>(P, rows, st);
+            default: return launch_sample_nv<NUC, float, 16>(P, rows, st);
         }
     }
     switch (nv) {
-        case 2: return launch_sample_nv<uint16_t, 2>(P, rows, st);
-        case 4: return launch_sample_nv<uint16_t, 4>(P, rows, st);
-        default: return launch_sample_nv<uint16_t, 8>(P, rows, st);
+        case 2: return launch_sample_nv<NUC, uint16_t, 2>(P, rows, st);
+        case 4: return launch_sample_nv<NUC, uint16_t, 4>(P, rows, st);
+        default: return launch_sample_nv<NUC, uint16_t, 8>(P, rows, st);
     }
+}
+
+hipError_t launch_sample(const SampleParams &P, int dtype, int nv, int rows, hipStream_t st) {
+    return launch_dispatch<false>(P, dtype, nv, rows, st);
+}
+
+hipError_t launch_nucleus(const SampleParams &P, int dtype, int nv, int rows, hipStream_t st) {
+    return launch_dispatch<true>(P, dtype, nv, rows, st);
 }
 
 }  // namespace zi
