@@ -367,33 +367,50 @@ __device__ __forceinline__ float owned_value(const RowSource &a, const PenTable 
 }
 
 // --------------------------------------------------------- stage A select
-// Candidate threshold tau <= the chunk's k-th largest value.  Each wave sorts
-// its 64 lane maxima (distinct elements of the chunk) and contributes its r
-// largest, r = max(ceil(k/W), 64/W); the union holds W*r >= k elements, so its
-// k-th largest is a lower bound of the chunk's k-th largest.  Lanes without a
-// value contribute okey(-inf) (harmless: a bound at -inf admits everything).
+// Candidate threshold tau <= the chunk's k-th largest value, from the lane
+// maxima (distinct elements of the chunk).  k <= 64: each wave sorts its 64
+// lane maxima and contributes its r largest, r = max(ceil(k/W), 64/W); the
+// union holds W*r >= k elements, so its k-th largest is a lower bound of the
+// chunk's k-th largest.  k > 64: every lane maximum enters the union (a
+// tighter bound than per-wave top-r lists), and wave 0 bisects the top 20
+// key bits for the largest T with at least k union keys >= T.  Lanes without
+// a value contribute okey(-inf) (a bound at -inf admits everything).
 // Penalized elements diverted from the stream are not in the union, which
 // only lowers the bound.  Contains two barriers.
-constexpr int kMaxR = kMaxTopK / kWaves;  // r for the largest k
-static_assert(kMaxR <= 64, "one sorted wave supplies r keys");
+constexpr int kMaxR = 64;  // union entries per wave
 
 __device__ __forceinline__ float chunk_tau(float m1, int k, uint32_t *uni, uint32_t *s_tau) {
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-    const int r = max((k + kWaves - 1) / kWaves, 64 / kWaves);
-    const uint32_t key = wave_sort_desc_u32((m1 == m1) ? okey(m1) : 0u);
-    if (lane < r) uni[wid * r + lane] = key;
+    const uint32_t mkey = (m1 == m1) ? okey(m1) : 0u;
+    if (k <= 64) {
+        const int r = max((k + kWaves - 1) / kWaves, 64 / kWaves);
+        const uint32_t key = wave_sort_desc_u32(mkey);
+        if (lane < r) uni[wid * r + lane] = key;
+    } else {
+        uni[tid] = mkey;
+    }
     __syncthreads();
     if (wid == 0) {
-        const int U = kWaves * r;
         uint32_t t;
-        if (U <= 64) {
+        if (k <= 64) {
+            const int U = kWaves * max((k + kWaves - 1) / kWaves, 64 / kWaves);
             const uint32_t u = wave_sort_desc_u32(lane < U ? uni[lane] : 0u);
             t = (uint32_t)__builtin_amdgcn_readlane((int)u, k - 1);
         } else {
-            uint32_t u4[4];
+            uint32_t u8[kWaves];
 #pragma unroll
-            for (int c = 0; c < 4; ++c) u4[c] = (lane + 64 * c < U) ? uni[lane + 64 * c] : 0u;
-            t = wave_kth_largest<4>(u4, k);
+            for (int c = 0; c < kWaves; ++c) u8[c] = uni[lane + 64 * c];
+            t = 0;
+            for (int b = 31; b >= 12; --b) {
+                const uint32_t cand = t | (1u << b);
+                int c = 0;
+#pragma unroll
+                for (int i = 0; i < kWaves; ++i) c += __popcll(ballot(u8[i] >= cand));
+                if (c >= k) t = cand;
+            }
+            // keys below okey(-inf) with the low bits cleared decode to NaN;
+            // no key lies in (0, okey(-inf)), so the count is unchanged
+            if (t != 0u && t < kNegInfKey) t = kNegInfKey;
         }
         if (lane == 0) *s_tau = t;
     }
@@ -529,7 +546,7 @@ constexpr int kWaveCand = 64;  // candidates per wave region
 template <typename T, int NV>
 struct SelectLds {
     static constexpr int VEC = VecTraits<T>::VEC;
-    uint32_t uni[kWaves * kMaxR];  // threshold union
+    uint32_t uni[kWaves * kMaxR];  // threshold union (all lane maxima for k > 64)
     float sx[kWaves][kStageCap * 2 * VEC];  // staged vector pairs
     uint32_t sid[kWaves][kStageCap * 2];
     uint64_t wkey[kWaves][kWaveCand];  // candidates, one region per wave
