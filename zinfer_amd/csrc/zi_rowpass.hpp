@@ -288,9 +288,17 @@ struct NoHook {
     __device__ void operator()(int, const float (&)[VEC], float) const {}
 };
 
-template <typename T, int NV, bool HAS_MASK, bool HAS_PEN, class Hook = NoHook>
+struct NoMid {
+    __device__ void operator()(float) const {}
+};
+
+// SPLIT < NV: after vector SPLIT-1 is processed, mid(partial lane max) runs
+// (the penalty hash is filled just before it) while the remaining vectors'
+// loads are still in flight; workgroup barriers inside mid order LDS only and
+// do not wait for them.
+template <typename T, int NV, bool HAS_MASK, bool HAS_PEN, class Hook = NoHook, int SPLIT = NV, class Mid = NoMid>
 __device__ __forceinline__ float chunk_stream(const RowSource &a, int row, int c0, int c1, ChunkRegs<T, NV> &cr,
-                                              PenTable *t, PenOwn *own, Hook hook = Hook()) {
+                                              PenTable *t, PenOwn *own, Hook hook = Hook(), Mid mid = Mid()) {
     constexpr int VEC = VecTraits<T>::VEC;
     const int tid = threadIdx.x;
     const int nvec = (c1 - c0 + VEC - 1) / VEC;
@@ -353,8 +361,12 @@ __device__ __forceinline__ float chunk_stream(const RowSource &a, int row, int c
         cr.m4[j] = m;
         tmax = fmaxf(tmax, m);
         hook.template operator()<VEC>(j, v, m);
+        if (SPLIT < NV && j == SPLIT - 1) {
+            if (HAS_PEN) pen_count(*t, rp, pr, c0, c1, *own);  // ordered by the barriers in mid
+            mid(tmax);
+        }
     }
-    if (HAS_PEN) pen_count(*t, rp, pr, c0, c1, *own);  // read by owners after the caller's next barrier
+    if (HAS_PEN && SPLIT >= NV) pen_count(*t, rp, pr, c0, c1, *own);  // read by owners after the caller's next barrier
     cr.lmax = tmax;
     return tmax;
 }
@@ -715,16 +727,25 @@ __device__ __forceinline__ void rank_count(const uint64_t *keys, const float *va
 // sorted by (value desc, id asc), publish it to `out` (agent-scope stores).
 // LDS: `sl` (SelectLds), `t` when HAS_PEN (with the owners in `own`), small
 // scalars.
-template <typename T, int NV, bool HAS_PEN>
+// The threshold comes from chunk_tau here, or (PRE_TAU) from select_prepare
+// run earlier, e.g. mid-stream on part of the chunk (a k-th largest of a
+// subset is still a lower bound).
+template <typename T, int NV>
+__device__ __forceinline__ float select_prepare(float lmax, int k, SelectLds<T, NV> &sl, uint32_t *s_tau, int *s_n) {
+    const int tid = threadIdx.x;
+    if (tid == 0) *s_n = 0;
+    if (tid < kSortMax) sl.rank[tid] = 0u;
+    return chunk_tau(lmax, k, sl.uni, s_tau);  // barriers: *s_n and rank settled
+}
+
+template <typename T, int NV, bool HAS_PEN, bool PRE_TAU = false>
 __device__ __forceinline__ void chunk_select_publish(const RowSource &a, ChunkRegs<T, NV> &cr, int c0, int k,
                                                      SelectLds<T, NV> &sl, const PenTable *t, const PenOwn *own,
                                                      uint32_t *s_tau, int *s_n, uint32_t *bins, int *s_dig,
-                                                     ChunkOut out) {
+                                                     ChunkOut out, float pre_tau = 0.0f) {
     constexpr int VEC = VecTraits<T>::VEC;
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-    if (tid == 0) *s_n = 0;
-    if (tid < kSortMax) sl.rank[tid] = 0u;
-    const float tau = chunk_tau(cr.lmax, k, sl.uni, s_tau);  // barriers: *s_n and rank settled
+    const float tau = PRE_TAU ? pre_tau : select_prepare<T, NV>(cr.lmax, k, sl, s_tau, s_n);
     const int wc = wave_candidates<T, NV, HAS_PEN>(a, cr, c0, tau, sl, t, own);
     if (lane == 0) sl.wcnt[wid] = wc;
     __syncthreads();

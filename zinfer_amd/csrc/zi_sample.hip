@@ -248,7 +248,12 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleParams P) {
     if constexpr (HAS_PEN) pen = &sm.a.p.pen;
     PenOwn own;
     ChunkRegs<T, NV> cr;
-    chunk_stream<T, NV, HAS_MASK, HAS_PEN>(a, row, c0, c1, cr, pen, &own);
+    // The candidate threshold is computed from the first kSplit vectors while
+    // the last ones are still arriving.
+    constexpr int kSplit = NV * 3 / 4;
+    float tau = 0.0f;
+    auto mid = [&](float lmax) { tau = select_prepare<T, NV>(lmax, k, sm.a.sel, s_tau, &s_n); };
+    chunk_stream<T, NV, HAS_MASK, HAS_PEN, NoHook, kSplit>(a, row, c0, c1, cr, pen, &own, NoHook(), mid);
     // This row's two uniforms, requested now so that the tail never waits
     // for them: a vector load (lane-varying index), issued after the row's
     // loads, which a scalar load's early wait would otherwise hold back.
@@ -257,7 +262,8 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleParams P) {
     const float u0 = P.uniforms[ur], u1 = P.uniforms[ur + 1];
     const int64_t rg = (int64_t)row * G + g;
     ChunkOut out{P.g_key + rg * kCapA, P.g_val + rg * kCapA, P.g_cnt + rg};
-    chunk_select_publish<T, NV, HAS_PEN>(a, cr, c0, k, sm.a.sel, pen, &own, s_tau, &s_n, s_bins, s_dig, out);
+    chunk_select_publish<T, NV, HAS_PEN, true>(a, cr, c0, k, sm.a.sel, pen, &own, s_tau, &s_n, s_bins, s_dig, out,
+                                               tau);
     if (!row_ticket(P.tickets, row, G, &s_flag)) return;
 
     // ---------------- stage B: the last workgroup of this row ----------------
