@@ -155,7 +155,9 @@ def main():
     rows_per_s = rows / (ms_per_step * 1e-3)
     nbytes = w.nbytes()
     achieved = nbytes / (ms_per_step * 1e-3) / 1e9
-    kernel = "sample_kernel"
+    top_k = w.params.get("top_k", 40)
+    k_eff = V if (top_k == 0 or top_k > V) else top_k
+    kernel = "nucleus_kernel" if k_eff > 256 else "sample_kernel"  # the launch's dominant kernel
     traffic = read_traffic(args.traffic, kernel, w.name)
 
     # sanity: every replayed batch reproduces the eager result of its set
