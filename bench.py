@@ -157,7 +157,12 @@ def main():
     achieved = nbytes / (ms_per_step * 1e-3) / 1e9
     top_k = w.params.get("top_k", 40)
     k_eff = V if (top_k == 0 or top_k > V) else top_k
-    kernel = "nucleus_kernel" if k_eff > 256 else "sample_kernel"  # the launch's dominant kernel
+    # the launch's dominant kernel: batches of >= 256 rows (kRowLoopRows in zi_sample.hip) run one
+    # workgroup per row
+    if rows >= 256:
+        kernel = "row_kernel"
+    else:
+        kernel = "nucleus_kernel" if k_eff > 256 else "sample_kernel"
     traffic = read_traffic(args.traffic, kernel, w.name)
 
     # sanity: every replayed batch reproduces the eager result of its set

@@ -137,3 +137,38 @@ def test_long_history_rows(ctx, oracle, H, win):
     o = oracle_sample(oracle, pk, x, u, hist, hist_len)
     errs = compare_sample(g, o, pk, V, f"hist{H}-win{win}")
     assert not errs, "\n".join(errs[:20])
+
+
+@pytest.mark.parametrize("rows,V,k,kind,pen,mask", [
+    (256, 20000, 50, "t3", True, False),
+    (300, 32000, 40, "normal", False, True),
+    (260, 131072, 256, "normal", True, False),
+    (256, 4099, 7, "ints", True, True),
+    (512, 17, 5, "flat", False, False),
+])
+def test_large_batch_rows(ctx, oracle, rows, V, k, kind, pen, mask):
+    """Batches of >= 256 rows run one workgroup per row (the running top-k
+    kept across the row's chunks)."""
+    rng = np.random.Generator(np.random.PCG64(rows * 7 + V))
+    x = _rows(rng, kind, rows, V)
+    u = rng.random((rows, 2), dtype=np.float32)
+    pk = dict(temp=0.8, top_k=k, top_p=0.9, min_p=0.05)
+    hist = hl = m = ei = ed = ec = None
+    if pen:
+        pk.update(repeat_penalty=1.2, freq_penalty=0.3, presence_penalty=0.4, penalty_last_n=128)
+        hist = rng.integers(0, V, (rows, 200), dtype=np.uint32)
+        hist[:, -8:] = np.argsort(-x, axis=1)[:, :8].astype(np.uint32)  # penalize some of the leaders
+        hl = rng.integers(0, 201, rows).astype(np.int32)
+        E = 8
+        ei = np.stack([rng.choice(V, size=min(E, V), replace=False).astype(np.uint32) for _ in range(rows)])
+        ed = (rng.random(ei.shape) * 2).astype(np.float32)
+        ec = rng.integers(0, ei.shape[1] + 1, rows).astype(np.int32)
+    if mask:
+        from zinfer_amd.workloads import pack_mask
+        bits = rng.random((rows, (V + 31) // 32 * 32)) < 0.5
+        bits[:, 0] = True
+        m = pack_mask(bits)
+    g = gpu_sample(ctx, pk, x, u, hist, hl, m, ei, ed, ec)
+    o = oracle_sample(oracle, pk, x, u, hist, hl, m, ei, ed, ec)
+    errs = compare_sample(g, o, pk, V, f"rows{rows}")
+    assert not errs, "\n".join(errs[:20])

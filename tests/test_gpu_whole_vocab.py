@@ -146,3 +146,19 @@ def test_config5_full_size_parity(ctx, oracle):
     o = oracle_sample(oracle, pk, w.logits, w.uniforms, w.hist, w.hist_len)
     errs = compare_sample(g, o, pk, w.vocab, w.name)
     assert not errs, "\n".join(errs[:20])
+
+
+@pytest.mark.parametrize("min_p,top_p", [(0.05, 0.98), (0.3, 0.9), (0.0, 0.98)])
+def test_whole_vocab_large_batch(ctx, oracle, min_p, top_p):
+    """>= 256 rows: the prefix pass runs one workgroup per row."""
+    V, rows = 32000, 256
+    rng = np.random.Generator(np.random.PCG64(int(min_p * 100) + int(top_p * 1000)))
+    x = _bf16_round((rng.standard_normal((rows, V)) * 3).astype(np.float32))
+    u = rng.random((rows, 2), dtype=np.float32)
+    hist = rng.integers(0, V, (rows, 128), dtype=np.uint32)
+    hl = np.full(rows, 128, np.int32)
+    pk = dict(temp=1.0, top_k=0, top_p=top_p, min_p=min_p, repeat_penalty=1.1, penalty_last_n=128)
+    g = gpu_sample(ctx, pk, x, u, hist, hl, bf16=True)
+    o = oracle_sample(oracle, pk, x, u, hist, hl)
+    errs = compare_sample(g, o, pk, V, f"wl{min_p}")
+    assert not errs, "\n".join(errs[:20])

@@ -15,6 +15,8 @@
 
 namespace zi {
 
+constexpr int kRowLoopRows = 256;  // batches this large run one workgroup per row
+
 template <bool P>
 struct PenLds {
     PenTable pen;
@@ -49,21 +51,28 @@ struct SampleStageB {
 // min-p cuts before kp_lo, or when kp_lo == kp_hi within the prefix; then the
 // rest of the tail only reads the prefix.  Lane 0 only; returns false when
 // the row needs the exact whole-order pass.
+// The row's total T = sum exp(x - mx) from the chunks' (max, sum) records.
+__device__ __forceinline__ double chunk_stats_total(const SampleParams &P, int row, float mx) {
+    const int G = P.src.G;
+    const double *gs = P.g_stat + (int64_t)row * G * 3;
+    double Mr = -INFINITY;
+    for (int g = 0; g < G; ++g) Mr = fmax(Mr, ld_agent(&gs[g * 3]));
+    double Z = 0.0;
+    for (int g = 0; g < G; ++g) {
+        const double m = ld_agent(&gs[g * 3]);
+        if (m != -INFINITY) Z += ld_agent(&gs[g * 3 + 1]) * exp(m - Mr);
+    }
+    return Z * exp(Mr - (double)mx);
+}
+
+// tot: the row's total when the caller has it (>= 0), else taken from the
+// chunk records.
 __device__ __forceinline__ bool nucleus_keep(const SampleParams &P, int row, const float *e, int n, int live,
-                                             int first_low, float mx, int &keep) {
+                                             int first_low, float mx, int &keep, double tot) {
     int kp_lo = n + 1, kp_hi = n + 1;  // n + 1: past the prefix
     if (P.top_p < 1.0f) {
         if (!__builtin_isfinite(mx)) return false;
-        const int G = P.src.G;
-        const double *gs = P.g_stat + (int64_t)row * G * 3;
-        double Mr = -INFINITY;
-        for (int g = 0; g < G; ++g) Mr = fmax(Mr, ld_agent(&gs[g * 3]));
-        double Z = 0.0;
-        for (int g = 0; g < G; ++g) {
-            const double m = ld_agent(&gs[g * 3]);
-            if (m != -INFINITY) Z += ld_agent(&gs[g * 3 + 1]) * exp(m - Mr);
-        }
-        const double T = Z * exp(Mr - (double)mx);
+        const double T = tot >= 0.0 ? tot : chunk_stats_total(P, row, mx);
         if (!(T >= 0.5 && T < 1e30)) return false;  // the term of the maximum alone is 1
         const double nu = (double)(P.n_all - 1) * 0x1p-24;
         const double gam = nu / (1.0 - nu) + 1e-4;
@@ -93,7 +102,7 @@ __device__ __forceinline__ bool nucleus_keep(const SampleParams &P, int row, con
 // its flag, and the candidate outputs cover the kept entries.
 template <bool NUC>
 __device__ __forceinline__ void sample_tail(const SampleParams &P, int row, const uint64_t *okey, const float *oval,
-                                            int n, TailLds &tl, float u0, float u1) {
+                                            int n, TailLds &tl, float u0, float u1, double tot = -1.0) {
     const int lane = threadIdx.x;
     float cv[4];
     uint32_t cid[4];
@@ -153,7 +162,7 @@ __device__ __forceinline__ void sample_tail(const SampleParams &P, int row, cons
     if (lane == 0) {
         int keep = n;
         if constexpr (NUC) {
-            settled0 = nucleus_keep(P, row, tl.e, n, live, first_low, mx, keep) ? 1 : 0;
+            settled0 = nucleus_keep(P, row, tl.e, n, live, first_low, mx, keep, tot) ? 1 : 0;
         } else {
             if (P.top_p < 1.0f) {  // :215-226
                 const float thr = P.top_p * lane_sum(tl.e, 0, live, 0.0f);
@@ -377,8 +386,159 @@ __global__ __launch_bounds__(kThreads) void nucleus_kernel(SampleParams P) {
     sample_tail<true>(P, row, sm.b.okey, sm.b.oval, n, sm.b.tl, u0, u1);
 }
 
+// Large batches: one workgroup per row loops over the row's G chunks and
+// keeps the running top-k sorted in LDS, so there is no cross-workgroup
+// handoff.  Each chunk is streamed and selected as in sample_kernel, with the
+// candidate threshold raised to the running k-th value once k entries are
+// held (elements below it cannot enter), its sorted list published to LDS,
+// and merged with the running list by rank (entries of the two lists are
+// distinct: each holds the count of greater entries of the other list by a
+// binary search).  NUC: the prefix pass of whole-vocabulary rows, with the
+// row total accumulated over the chunks in each thread.
+struct RowLoopLds {
+    uint64_t key[2][kCapA];  // running list, double-buffered
+    float val[2][kCapA];
+    uint64_t bk[kCapA];      // this chunk's list
+    float bv[kCapA];
+    int32_t bn;
+};
+
+// Entries of the sorted-descending list L[0, n) greater than `mine`.
+__device__ __forceinline__ int count_greater_n(const uint64_t *L, int n, uint64_t mine) {
+    int lo = 0, hi = n;  // L[i] > mine for i < lo, L[i] <= mine for i >= hi
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (L[mid] > mine) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
+
+template <typename T, int NV, bool HAS_MASK, bool HAS_PEN, bool NUC>
+__global__ __launch_bounds__(kThreads) void row_kernel(SampleParams P) {
+    __shared__ union {
+        SampleStageA<T, NV, HAS_PEN> a;
+        TailLds tl;
+    } sm;
+    __shared__ RowLoopLds rl;
+    __shared__ uint32_t s_bins[256];
+    __shared__ uint32_t s_tau[1];
+    __shared__ int s_dig[2];
+    __shared__ int s_n;
+    __shared__ float s_wmax[kWaves];
+    __shared__ double s_ws[kWaves];
+
+    const RowSource &a = P.src;
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int G = a.G;
+    const int row = blockIdx.x;
+    const int k = P.k;
+    int ur = 2 * row;
+    asm volatile("" : "+v"(ur));
+    const float u0 = P.uniforms[ur], u1 = P.uniforms[ur + 1];
+
+    PenTable *pen = nullptr;
+    if constexpr (HAS_PEN) pen = &sm.a.p.pen;
+    float ref = -INFINITY, S = 0.0f;  // NUC: running sum exp(x - ref) of this thread's elements
+    int n_run = 0, cur = 0;           // running list length and buffer (uniform)
+    for (int g = 0; g < G; ++g) {
+        const int c0 = g * a.CH;
+        const int c1 = min(a.V, c0 + a.CH);
+        PenOwn own;
+        ChunkRegs<T, NV> cr;
+        chunk_stream<T, NV, HAS_MASK, HAS_PEN>(a, row, c0, c1, cr, pen, &own);
+        float tau = select_prepare<T, NV>(cr.lmax, k, sm.a.sel, s_tau, &s_n);
+        if (n_run == k) tau = fmaxf(tau, okey_inv((uint32_t)(rl.key[cur][k - 1] >> 32)));
+        chunk_select_publish<T, NV, HAS_PEN, true>(a, cr, c0, k, sm.a.sel, pen, &own, s_tau, &s_n, s_bins, s_dig,
+                                                   ChunkOut{rl.bk, rl.bv, &rl.bn}, tau);
+        if constexpr (NUC) {  // this chunk's elements, penalized ones from their owners
+            constexpr int VEC = VecTraits<T>::VEC;
+            float m = cr.lmax;
+            if constexpr (HAS_PEN) {
+#pragma unroll
+                for (int u = 0; u < kOwnSlots; ++u)
+                    if (own.id[u] != 0xFFFFFFFFu) m = fmaxf(m, owned_value(a, *pen, own, u));
+            }
+            if (m > ref) {
+                S = (ref == -INFINITY) ? 0.0f : S * __builtin_amdgcn_exp2f((ref - m) * kLog2e);
+                ref = m;
+            }
+            if (ref != -INFINITY) {
+#pragma unroll
+                for (int i = 0; i < NV * VEC; ++i)
+                    S = S + __builtin_amdgcn_exp2f(fmaxf(cr.x[i] - ref, -200.0f) * kLog2e);
+                if constexpr (HAS_PEN) {
+#pragma unroll
+                    for (int u = 0; u < kOwnSlots; ++u)
+                        if (own.id[u] != 0xFFFFFFFFu)
+                            S = S + __builtin_amdgcn_exp2f(fmaxf(owned_value(a, *pen, own, u) - ref, -200.0f) * kLog2e);
+                }
+            }
+        }
+        __syncthreads();  // the chunk's list is in rl.bk / rl.bv / rl.bn
+        const int nb = rl.bn;
+        const int nxt = cur ^ 1;
+        if (tid < n_run) {
+            const uint64_t mine = rl.key[cur][tid];
+            const int r = tid + count_greater_n(rl.bk, nb, mine);
+            if (r < k) {
+                rl.key[nxt][r] = mine;
+                rl.val[nxt][r] = rl.val[cur][tid];
+            }
+        } else if (tid >= kCapA && tid - kCapA < nb) {
+            const int i = tid - kCapA;
+            const uint64_t mine = rl.bk[i];
+            const int r = i + count_greater_n(rl.key[cur], n_run, mine);
+            if (r < k) {
+                rl.key[nxt][r] = mine;
+                rl.val[nxt][r] = rl.bv[i];
+            }
+        }
+        n_run = min(k, n_run + nb);
+        cur = nxt;
+        __syncthreads();  // the running list is complete; stage-A LDS may be reused
+    }
+
+    double tot = -1.0;
+    if constexpr (NUC) {  // the row total from every thread's (ref, S)
+        const float wm = wave_max_f(ref);
+        if (lane == 0) s_wmax[wid] = wm;
+        __syncthreads();
+        float M = s_wmax[0];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) M = fmaxf(M, s_wmax[w]);
+        double ds = (ref != -INFINITY && M != -INFINITY) ? (double)S * exp((double)ref - (double)M) : 0.0;
+        ds = wave_sum_d(ds);
+        if (lane == 0) s_ws[wid] = ds;
+        __syncthreads();
+        double Z = 0.0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) Z += s_ws[w];
+        tot = (n_run > 0) ? Z * exp((double)M - (double)rl.val[cur][0]) : 0.0;
+    }
+    if (tid >= 64) return;  // the tail runs on wave 0 with all 64 lanes active
+    if (n_run == 0) {
+        if (tid == 0) {
+            if constexpr (NUC) {
+                P.nuc_flag[row] = 1;
+            } else {
+                P.tok[row] = 0u;
+                P.margin[row] = 10.0f;
+                if (P.ndraws) P.ndraws[row] = 0;
+                if (P.keep) P.keep[row] = 0;
+            }
+        }
+        return;
+    }
+    sample_tail<NUC>(P, row, rl.key[cur], rl.val[cur], n_run, sm.tl, u0, u1, tot);
+}
+
 template <bool NUC, typename T, int NV, bool M, bool PN>
 static hipError_t launch_sample_t(const SampleParams &P, int rows, hipStream_t st) {
+    if (rows >= kRowLoopRows) {  // one workgroup per row fills the device
+        hipLaunchKernelGGL((row_kernel<T, NV, M, PN, NUC>), dim3(rows), dim3(kThreads), 0, st, P);
+        return hipGetLastError();
+    }
     dim3 grid(rows * P.src.G), block(kThreads);
     if constexpr (NUC) hipLaunchKernelGGL((nucleus_kernel<T, NV, M, PN>), grid, block, 0, st, P);
     else hipLaunchKernelGGL((sample_kernel<T, NV, M, PN>), grid, block, 0, st, P);
