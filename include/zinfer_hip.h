@@ -169,6 +169,58 @@ int32_t zi_entropy_topk_rows(zi_ctx *ctx, const zi_batch *b, int32_t k, const ui
  * Only logits, dtype, rows, vocab, ld, mask, mask_ld of `b` are read. */
 int32_t zi_apply_mask_rows(zi_ctx *ctx, const zi_batch *b);
 
+/* ------------------------------------------------ JSON grammar mask (GPU) */
+
+/* JsonValidator (src/grammar.zig:59-68) as plain data.  state / escape / num
+ * are the positions in State, EscapeState and NumState (:13-57); bit d of
+ * stack is 1 when stack[d] is .array, 0 for .object (d < depth <= 64). */
+typedef struct zi_json_state {
+    uint64_t stack;
+    uint8_t  state;
+    uint8_t  escape;
+    uint8_t  num;
+    uint8_t  depth;
+    uint8_t  lit_len;
+    uint8_t  lit_idx;
+    uint8_t  object_only;     /* is_object_only */
+    uint8_t  reserved;
+    uint8_t  lit_expected[8];
+} zi_json_state;
+
+/* Host state machine, same semantics as the reference. */
+void    zi_json_init(zi_json_state *s, int32_t object_only);           /* initObjectOnly / initAny :70-76 */
+int32_t zi_json_is_finished(const zi_json_state *s);                   /* isFinished :78-80 */
+int32_t zi_json_step_byte(zi_json_state *s, uint8_t b);                /* stepByte :195-381 */
+/* consume (:437-443): in place; on failure the bytes before the bad one stay
+ * applied.  Returns 1 / 0. */
+int32_t zi_json_consume(zi_json_state *s, const uint8_t *piece, size_t n);
+/* tryConsume (:428-434): 1 and *out = the new state, or 0 (out untouched). */
+int32_t zi_json_try_consume(const zi_json_state *s, const uint8_t *piece, size_t n, zi_json_state *out);
+
+/* The token pieces on the device: Tokenizer.piece_off [V+1] / piece_buf
+ * (decoded bytes of every token, src/tokenizer.zig:35-36, piece() :274-276),
+ * the end-of-generation ids (Tokenizer.eog, isEog :270-272) and the eos id
+ * every reference call site passes to applyMask (g.tok.eos, src/gen.zig:458;
+ * -1 for none).  Host arrays, copied (synchronous).  cache_states > 0 keeps
+ * that many per-state masks on the device (least recently used replaced). */
+typedef struct zi_vocab zi_vocab;
+int32_t zi_vocab_create(zi_vocab **out, zi_ctx *ctx, const uint32_t *piece_off, const uint8_t *piece_buf,
+                        uint32_t n_vocab, const uint32_t *eog, uint32_t n_eog, int64_t eos,
+                        int32_t cache_states);
+void    zi_vocab_destroy(zi_vocab *v);
+
+/* JsonValidator.applyMask (src/grammar.zig:446-479) as a packed mask, one
+ * row per validator state: bit t of out_mask[r][t >> 5] is set when the
+ * reference leaves logit t unchanged (the layout zi_batch.mask reads); bits
+ * at and above V are clear.  states: host [rows]; out_mask: device
+ * [rows][mask_ld], mask_ld >= ceil(V / 32).  Stream-ordered. */
+int32_t zi_json_mask_rows(zi_ctx *ctx, zi_vocab *v, const zi_json_state *states, int32_t rows,
+                          uint32_t *out_mask, int32_t mask_ld);
+
+/* applyMask on one host row, in place (the reference signature): logits of
+ * disallowed tokens become -inf.  Synchronous. */
+int32_t zi_json_apply_mask(zi_ctx *ctx, zi_vocab *v, const zi_json_state *s, float *logits, uint32_t n);
+
 /* ------------------------------------------ host mirror of the Zig Sampler */
 
 /* The Sampler of src/sampler.zig:38-286 with the same state (params, RNG,

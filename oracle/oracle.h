@@ -28,6 +28,11 @@
  *   or_apply_mask          pinned: closed form (bit test -> -inf).
  *   or_entropy_topk        pinned: scipy.stats.entropy(softmax) and brute-force top-k.
  *   or_adaptive_*          pinned: reference KAT gen.zig:845-874.
+ *   or_json_*              pinned: reference KATs grammar.zig:482-513; json.dumps
+ *                          documents are accepted with every prefix; every text
+ *                          accepted to the finished state parses with json.loads;
+ *                          hand-derived byte tables per state (the \\u quirk, the
+ *                          depth-64 limit, object-only roots).
  *   or_rng_*               PARITY UNPINNED for the Zig DefaultPrng stream (no Zig
  *                          here, no reference vectors); splitmix64 alone is pinned
  *                          by its published sequence for seed 1234567.
@@ -159,6 +164,33 @@ double or_bench_sample_rows(const or_params *p, const float *logits, uint32_t ro
                             uint32_t hist_ld, const uint32_t *mask, uint32_t mask_ld,
                             const float *uniforms, uint32_t reps, uint32_t *out_tok,
                             float *out_margin);
+
+/* JsonValidator, src/grammar.zig:59-480 (grammar_oracle.c).  Fields follow
+ * the reference: state / escape / num are the enum positions of State,
+ * EscapeState and NumState (:13-57); stack[d] is 0 for .object, 1 for .array. */
+typedef struct or_json {
+    int32_t state;
+    int32_t escape;
+    int32_t num;
+    uint32_t depth;
+    uint8_t stack[64];
+    uint8_t lit_expected[8];
+    uint8_t lit_len;
+    uint8_t lit_idx;
+    uint8_t object_only;
+    uint8_t pad_;
+} or_json;
+
+void   or_json_init(or_json *j, int object_only);
+int    or_json_is_finished(const or_json *j);
+int    or_json_step_byte(or_json *j, uint8_t b);
+int    or_json_try_consume(const or_json *j, const uint8_t *piece, size_t n, or_json *out);
+int    or_json_consume(or_json *j, const uint8_t *piece, size_t n);
+void   or_json_mask(const or_json *j, const uint32_t *piece_off, const uint8_t *piece_buf, uint32_t V,
+                    const uint32_t *eog, uint32_t n_eog, int64_t eos, uint32_t *out);
+double or_bench_json_mask(const or_json *states, uint32_t rows, const uint32_t *piece_off,
+                          const uint8_t *piece_buf, uint32_t V, const uint32_t *eog, uint32_t n_eog,
+                          int64_t eos, uint32_t *out, uint32_t reps);
 
 #ifdef __cplusplus
 }

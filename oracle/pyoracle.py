@@ -55,6 +55,22 @@ class OrDiag(C.Structure):
     ]
 
 
+class OrJson(C.Structure):
+    """JsonValidator state, src/grammar.zig:59-68 (see or_json in oracle.h)."""
+    _fields_ = [
+        ("state", C.c_int32),
+        ("escape", C.c_int32),
+        ("num", C.c_int32),
+        ("depth", C.c_uint32),
+        ("stack", C.c_uint8 * 64),
+        ("lit_expected", C.c_uint8 * 8),
+        ("lit_len", C.c_uint8),
+        ("lit_idx", C.c_uint8),
+        ("object_only", C.c_uint8),
+        ("pad_", C.c_uint8),
+    ]
+
+
 class OrAdaptive(C.Structure):
     _fields_ = [
         ("cur_k", C.c_uint64),
@@ -116,6 +132,17 @@ def lib():
         L.or_bench_sample_rows.argtypes = [C.POINTER(OrParams), f32p, C.c_uint32, C.c_uint32, C.c_uint64,
                                            u32p, C.POINTER(C.c_int32), C.c_uint32, u32p, C.c_uint32,
                                            f32p, C.c_uint32, u32p, f32p]
+        jp = C.POINTER(OrJson)
+        u8p = C.POINTER(C.c_uint8)
+        L.or_json_init.argtypes = [jp, C.c_int]
+        L.or_json_is_finished.argtypes = [jp]
+        L.or_json_step_byte.argtypes = [jp, C.c_uint8]
+        L.or_json_try_consume.argtypes = [jp, u8p, C.c_size_t, jp]
+        L.or_json_consume.argtypes = [jp, u8p, C.c_size_t]
+        L.or_json_mask.argtypes = [jp, u32p, u8p, C.c_uint32, u32p, C.c_uint32, C.c_int64, u32p]
+        L.or_bench_json_mask.restype = C.c_double
+        L.or_bench_json_mask.argtypes = [jp, C.c_uint32, u32p, u8p, C.c_uint32, u32p, C.c_uint32, C.c_int64,
+                                         u32p, C.c_uint32]
         _lib = L
     return _lib
 
@@ -253,3 +280,76 @@ def bench_sample_rows(p: OrParams, logits2d, hist, hist_len, mask, uniforms, rep
                                    _p(mk, C.c_uint32), 0 if mk is None else mk.shape[1],
                                    _p(u, C.c_float), reps, _p(tok, C.c_uint32), _p(mar, C.c_float))
     return t, tok, mar
+
+
+# ---------------------------------------------------------------- grammar
+
+
+def json_init(object_only: bool = True) -> OrJson:
+    """JsonValidator.initObjectOnly / initAny (src/grammar.zig:70-76)."""
+    j = OrJson()
+    lib().or_json_init(C.byref(j), int(bool(object_only)))
+    return j
+
+
+def json_copy(j: OrJson) -> OrJson:
+    c = OrJson()
+    C.memmove(C.byref(c), C.byref(j), C.sizeof(OrJson))
+    return c
+
+
+def json_is_finished(j: OrJson) -> bool:
+    return bool(lib().or_json_is_finished(C.byref(j)))
+
+
+def _bytes(piece) -> tuple:
+    b = piece.encode() if isinstance(piece, str) else bytes(piece)
+    buf = (C.c_uint8 * max(len(b), 1)).from_buffer_copy(b or b"\0")
+    return buf, len(b)
+
+
+def json_consume(j: OrJson, piece) -> bool:
+    """consume (src/grammar.zig:437-443): in place."""
+    buf, n = _bytes(piece)
+    return bool(lib().or_json_consume(C.byref(j), buf, n))
+
+
+def json_try_consume(j: OrJson, piece):
+    """tryConsume (src/grammar.zig:428-434): the new state, or None."""
+    buf, n = _bytes(piece)
+    out = OrJson()
+    ok = lib().or_json_try_consume(C.byref(j), buf, n, C.byref(out))
+    return out if ok else None
+
+
+def json_mask(j: OrJson, piece_off, piece_buf, eog=(), eos=None) -> np.ndarray:
+    """applyMask (src/grammar.zig:446-479) as the packed allowed-token mask."""
+    off = np.ascontiguousarray(piece_off, dtype=np.uint32)
+    buf = np.ascontiguousarray(piece_buf, dtype=np.uint8)
+    if buf.size == 0:
+        buf = np.zeros(1, np.uint8)
+    V = off.size - 1
+    e = np.ascontiguousarray(np.asarray(eog, dtype=np.uint32).reshape(-1))
+    if e.size == 0:
+        e = np.zeros(1, np.uint32)
+        ne = 0
+    else:
+        ne = e.size
+    out = np.zeros((V + 31) // 32, np.uint32)
+    lib().or_json_mask(C.byref(j), _p(off, C.c_uint32), _p(buf, C.c_uint8), V, _p(e, C.c_uint32), ne,
+                       -1 if eos is None else int(eos), _p(out, C.c_uint32))
+    return out
+
+
+def bench_json_mask(states, piece_off, piece_buf, eog, eos, reps: int):
+    """Seconds for `reps` passes of json_mask over every state."""
+    arr = (OrJson * len(states))(*states)
+    off = np.ascontiguousarray(piece_off, dtype=np.uint32)
+    buf = np.ascontiguousarray(piece_buf, dtype=np.uint8)
+    e = np.ascontiguousarray(np.asarray(eog, dtype=np.uint32).reshape(-1))
+    V = off.size - 1
+    out = np.zeros((len(states), (V + 31) // 32), np.uint32)
+    t = lib().or_bench_json_mask(arr, len(states), _p(off, C.c_uint32), _p(buf, C.c_uint8), V,
+                                 _p(e, C.c_uint32), e.size, -1 if eos is None else int(eos),
+                                 _p(out, C.c_uint32), reps)
+    return t, out

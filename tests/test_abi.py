@@ -36,7 +36,7 @@ def test_struct_layout_matches_header(tmp_path):
     from zinfer_amd import _lib
 
     structs = {"zi_params": _lib.ZiParams, "zi_batch": _lib.ZiBatch, "zi_sample_out": _lib.ZiSampleOut,
-               "zi_adaptive_draft": _lib.ZiAdaptiveDraft}
+               "zi_adaptive_draft": _lib.ZiAdaptiveDraft, "zi_json_state": _lib.ZiJsonState}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "zinfer_hip.h"', "int main(void) {"]
     for name, cls in structs.items():
         lines.append(f'printf("{name} size %zu\\n", sizeof({name}));')

@@ -90,6 +90,25 @@ class ZiAdaptiveDraft(C.Structure):
     ]
 
 
+class ZiJsonState(C.Structure):
+    """JsonValidator state (src/grammar.zig:59-68); see zi_json_state."""
+    _fields_ = [
+        ("stack", C.c_uint64),
+        ("state", C.c_uint8),
+        ("escape", C.c_uint8),
+        ("num", C.c_uint8),
+        ("depth", C.c_uint8),
+        ("lit_len", C.c_uint8),
+        ("lit_idx", C.c_uint8),
+        ("object_only", C.c_uint8),
+        ("reserved", C.c_uint8),
+        ("lit_expected", C.c_uint8 * 8),
+    ]
+
+
+u8p = C.POINTER(C.c_uint8)
+jsp = C.POINTER(ZiJsonState)
+
 # name -> (restype, argtypes); mirrors include/zinfer_hip.h one to one
 SIGNATURES = {
     "zi_params_default": (None, [C.POINTER(ZiParams)]),
@@ -106,6 +125,16 @@ SIGNATURES = {
     "zi_entropy_topk_rows": (C.c_int32, [C.c_void_p, C.POINTER(ZiBatch), C.c_int32, C.c_void_p, C.c_void_p,
                                           C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p]),
     "zi_apply_mask_rows": (C.c_int32, [C.c_void_p, C.POINTER(ZiBatch)]),
+    "zi_json_init": (None, [jsp, C.c_int32]),
+    "zi_json_is_finished": (C.c_int32, [jsp]),
+    "zi_json_step_byte": (C.c_int32, [jsp, C.c_uint8]),
+    "zi_json_consume": (C.c_int32, [jsp, u8p, C.c_size_t]),
+    "zi_json_try_consume": (C.c_int32, [jsp, u8p, C.c_size_t, jsp]),
+    "zi_vocab_create": (C.c_int32, [C.POINTER(C.c_void_p), C.c_void_p, u32p, u8p, C.c_uint32, u32p, C.c_uint32,
+                                     C.c_int64, C.c_int32]),
+    "zi_vocab_destroy": (None, [C.c_void_p]),
+    "zi_json_mask_rows": (C.c_int32, [C.c_void_p, C.c_void_p, jsp, C.c_int32, C.c_void_p, C.c_int32]),
+    "zi_json_apply_mask": (C.c_int32, [C.c_void_p, C.c_void_p, jsp, f32p, C.c_uint32]),
     "zi_sampler_init": (C.c_int32, [C.POINTER(C.c_void_p), C.c_void_p, C.c_uint32, C.POINTER(ZiParams)]),
     "zi_sampler_deinit": (None, [C.c_void_p]),
     "zi_sampler_reset": (None, [C.c_void_p]),

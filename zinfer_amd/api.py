@@ -15,7 +15,7 @@ import torch
 from . import _lib
 from ._lib import ZiBatch, ZiParams, ZiSampleOut, check, lib
 
-__all__ = ["Context", "Sampler", "params", "SampleResult"]
+__all__ = ["Context", "Sampler", "params", "SampleResult", "JsonValidator", "Vocab"]
 
 params = _lib.params
 
@@ -207,3 +207,98 @@ class Sampler:
 
     def set_params(self, p: ZiParams):
         lib().zi_sampler_set_params(self.h, C.byref(p))
+
+
+def _piece(piece):
+    b = piece.encode() if isinstance(piece, str) else bytes(piece)
+    return (C.c_uint8 * max(len(b), 1)).from_buffer_copy(b or b"\0"), len(b)
+
+
+class JsonValidator:
+    """The reference's JsonValidator (src/grammar.zig:59-480) over the C ABI:
+    the host state machine (zi_json_*) and the GPU mask (Vocab.json_mask_rows)."""
+
+    def __init__(self, object_only: bool = True):
+        self.st = _lib.ZiJsonState()
+        lib().zi_json_init(C.byref(self.st), int(bool(object_only)))
+
+    @classmethod
+    def init_object_only(cls) -> "JsonValidator":  # :70-72
+        return cls(True)
+
+    @classmethod
+    def init_any(cls) -> "JsonValidator":  # :74-76
+        return cls(False)
+
+    def copy(self) -> "JsonValidator":
+        c = JsonValidator.__new__(JsonValidator)
+        c.st = _lib.ZiJsonState()
+        C.memmove(C.byref(c.st), C.byref(self.st), C.sizeof(_lib.ZiJsonState))
+        return c
+
+    def is_finished(self) -> bool:  # :78-80
+        return bool(lib().zi_json_is_finished(C.byref(self.st)))
+
+    def step_byte(self, b: int) -> bool:  # :195-381
+        return bool(lib().zi_json_step_byte(C.byref(self.st), int(b)))
+
+    def consume(self, piece) -> bool:  # :437-443
+        buf, n = _piece(piece)
+        return bool(lib().zi_json_consume(C.byref(self.st), buf, n))
+
+    def try_consume(self, piece) -> Optional["JsonValidator"]:  # :428-434
+        buf, n = _piece(piece)
+        out = JsonValidator.__new__(JsonValidator)
+        out.st = _lib.ZiJsonState()
+        return out if lib().zi_json_try_consume(C.byref(self.st), buf, n, C.byref(out.st)) else None
+
+    def apply_mask(self, logits, vocab: "Vocab"):  # :446-479, host logits in place
+        import numpy as np
+        assert isinstance(logits, np.ndarray) and logits.dtype == np.float32 and logits.flags.c_contiguous
+        check(lib().zi_json_apply_mask(vocab.ctx.h, vocab.h, C.byref(self.st), logits.ctypes.data_as(_lib.f32p),
+                                       logits.size))
+        return logits
+
+
+class Vocab:
+    """Token pieces on the device (zi_vocab): Tokenizer.piece_off / piece_buf,
+    the end-of-generation ids and the eos id (src/tokenizer.zig:35-47)."""
+
+    def __init__(self, ctx: Context, piece_off, piece_buf, eog=(), eos=None, cache_states: int = 64):
+        import numpy as np
+        self.ctx = ctx
+        self.h = None
+        off = np.ascontiguousarray(piece_off, dtype=np.uint32)
+        buf = np.ascontiguousarray(piece_buf, dtype=np.uint8)
+        if buf.size == 0:
+            buf = np.zeros(1, np.uint8)
+        e = np.ascontiguousarray(np.asarray(eog, dtype=np.uint32).reshape(-1))
+        self.V = off.size - 1
+        self.words = (self.V + 31) // 32
+        h = C.c_void_p()
+        check(lib().zi_vocab_create(C.byref(h), ctx.h, off.ctypes.data_as(_lib.u32p), buf.ctypes.data_as(_lib.u8p),
+                                    self.V, e.ctypes.data_as(_lib.u32p) if e.size else None, e.size,
+                                    -1 if eos is None else int(eos), cache_states))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().zi_vocab_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def json_mask_rows(self, validators, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Packed allowed-token masks [rows][ceil(V/32)] (int32 view of u32), one row per validator."""
+        rows = len(validators)
+        arr = (_lib.ZiJsonState * rows)(*[v.st for v in validators])
+        if out is None:
+            out = torch.empty((rows, self.words), dtype=torch.int32, device=f"cuda:{self.ctx.device}")
+        assert out.dtype == torch.int32 and out.is_cuda and out.shape[0] >= rows and out.stride(1) == 1
+        self.ctx._bind_stream()
+        check(lib().zi_json_mask_rows(self.ctx.h, self.h, arr, rows, _ptr(out), out.stride(0)))
+        return out

@@ -1,0 +1,253 @@
+// JSON validator state machine (src/grammar.zig:59-443), shared by the host
+// entry points (consume after a token is accepted, src/gen.zig:624) and the
+// mask kernel (one lane per token piece).  The 64-entry container stack is a
+// bit word: bit d set means stack[d] == .array.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+
+#include "zinfer_hip.h"
+
+namespace zi {
+
+// State, EscapeState, NumState in declaration order (src/grammar.zig:13-57).
+enum : uint32_t {
+    kJStart, kJKeyOrClose, kJKeyOnly, kJInKey, kJColon, kJValue,
+    kJArrValOrClose, kJInStr, kJInNum, kJInLit, kJCommaOrClose, kJFinished, kJStates
+};
+enum : uint32_t { kEscNone, kEscEscaped, kEscHex1, kEscHex2, kEscHex3, kEscHex4 };
+enum : uint32_t { kNumMinus, kNumZero, kNumInt, kNumDot, kNumFrac, kNumExp, kNumExpSign, kNumExpDigits };
+constexpr uint32_t kJsonMaxDepth = 64;  // JsonValidator.stack: [64]ContainerType
+// Inside the machine, State.inside_num with NumState n is the one state
+// kJNum + n, so that every transition writes a single state variable.
+constexpr uint32_t kJNum = kJStates;
+
+struct JsonFsm {
+    uint64_t stack;
+    uint64_t lit;  // lit_expected, byte i at bits 8i
+    uint32_t state, escape, num, depth, lit_len, lit_idx, object_only;  // num: the last NumState
+
+    __host__ __device__ static bool ws(uint32_t b) { return b == ' ' || b == '\t' || b == '\n' || b == '\r'; }
+    __host__ __device__ static bool digit(uint32_t b) { return b - '0' < 10u; }
+    __host__ __device__ static bool hex(uint32_t b) {  // isHex, :55-57
+        return digit(b) || (b | 0x20u) - 'a' < 6u;
+    }
+
+    __host__ __device__ void load(const zi_json_state &s) {
+        stack = s.stack;
+        memcpy(&lit, s.lit_expected, 8);  // little-endian: byte i at bits 8i
+        state = s.state == kJInNum ? kJNum + s.num : s.state;
+        escape = s.escape;
+        num = s.num;
+        depth = s.depth;
+        lit_len = s.lit_len;
+        lit_idx = s.lit_idx;
+        object_only = s.object_only;
+    }
+    __host__ __device__ void store(zi_json_state &s) const {
+        s.stack = stack;
+        memcpy(s.lit_expected, &lit, 8);
+        s.state = (uint8_t)(state >= kJNum ? kJInNum : state);
+        s.escape = (uint8_t)escape;
+        s.num = (uint8_t)(state >= kJNum ? state - kJNum : num);
+        s.depth = (uint8_t)depth;
+        s.lit_len = (uint8_t)lit_len;
+        s.lit_idx = (uint8_t)lit_idx;
+        s.object_only = (uint8_t)object_only;
+    }
+
+    __host__ __device__ bool finished() const { return state == kJFinished && depth == 0; }  // :78-80
+
+    __host__ __device__ bool push(bool array, uint32_t next) {
+        if (depth >= kJsonMaxDepth) return false;
+        const uint64_t bit = 1ull << depth;
+        stack = array ? (stack | bit) : (stack & ~bit);
+        depth += 1;
+        state = next;
+        return true;
+    }
+    __host__ __device__ bool top_is_array() const { return (stack >> (depth - 1)) & 1ull; }
+
+    // stepString (:82-132): a \u escape ends after three hex digits (hex3
+    // returns to none; hex4 is never entered).
+    __host__ __device__ bool step_string(uint32_t b, uint32_t next) {
+        switch (escape) {
+        case kEscNone:
+            if (b == '\\') { escape = kEscEscaped; return true; }
+            if (b == '"') { state = next; return true; }
+            return b >= 0x20;
+        case kEscEscaped:
+            if (b == '"' || b == '\\' || b == '/' || b == 'b' || b == 'f' || b == 'n' || b == 'r' || b == 't') {
+                escape = kEscNone;
+                return true;
+            }
+            if (b == 'u') { escape = kEscHex1; return true; }
+            return false;
+        case kEscHex1:
+        case kEscHex2:
+        case kEscHex3:
+            if (!hex(b)) return false;
+            escape = escape == kEscHex3 ? kEscNone : escape + 1;
+            return true;
+        default:
+            return false;
+        }
+    }
+
+    __host__ __device__ void literal(uint64_t word, uint32_t len) {
+        lit = word;
+        lit_len = len;
+        lit_idx = 1;
+        state = kJInLit;
+    }
+
+    // stepValueStart (:134-192)
+    __host__ __device__ bool value_start(uint32_t b) {
+        if (b == '"') { escape = kEscNone; state = kJInStr; return true; }
+        if (b == '{') return push(false, kJKeyOrClose);
+        if (b == '[') return push(true, kJArrValOrClose);
+        if (b == '-') { state = kJNum + kNumMinus; return true; }
+        if (b == '0') { state = kJNum + kNumZero; return true; }
+        if (b - '1' < 9u) { state = kJNum + kNumInt; return true; }
+        if (b == 't') { literal(0x65757274ull, 4); return true; }    // "true"
+        if (b == 'f') { literal(0x65736c6166ull, 5); return true; }  // "false"
+        if (b == 'n') { literal(0x6c6c756eull, 4); return true; }    // "null"
+        return false;
+    }
+
+    // transitionComma (:398-408) / transitionClose (:410-425)
+    __host__ __device__ bool comma() {
+        if (depth == 0) return false;
+        state = top_is_array() ? kJValue : kJKeyOnly;
+        return true;
+    }
+    __host__ __device__ bool close(uint32_t b) {
+        if (depth == 0) return false;
+        if ((b == ']') != top_is_array()) return false;
+        depth -= 1;
+        state = depth == 0 ? kJFinished : kJCommaOrClose;
+        return true;
+    }
+    // stepNumDelimiter (:383-396) from a NumState that canTerminate (:47-52):
+    // the callers are the zero, int_digits, frac_digits and exp_digits states.
+    __host__ __device__ bool num_delim(uint32_t b, uint32_t n) {
+        num = n;  // the reference keeps num_state after the number ends
+        if (ws(b)) { state = kJCommaOrClose; return true; }
+        if (b == ',') return comma();
+        if (b == '}' || b == ']') return close(b);
+        return false;
+    }
+
+    // stepByte (:195-381)
+    __host__ __device__ bool step(uint32_t b) {
+        switch (state) {
+        case kJStart:
+            if (ws(b)) return true;
+            if (b == '{') return push(false, kJKeyOrClose);
+            if (!object_only && b == '[') return push(true, kJArrValOrClose);
+            return false;
+        case kJKeyOrClose:
+            if (ws(b)) return true;
+            if (b == '}') {  // the '{' just read is on the stack: depth >= 1
+                if (depth == 0) return false;
+                depth -= 1;
+                state = depth == 0 ? kJFinished : kJCommaOrClose;
+                return true;
+            }
+            if (b == '"') { escape = kEscNone; state = kJInKey; return true; }
+            return false;
+        case kJKeyOnly:
+            if (ws(b)) return true;
+            if (b == '"') { escape = kEscNone; state = kJInKey; return true; }
+            return false;
+        case kJInKey:
+            return step_string(b, kJColon);
+        case kJColon:
+            if (ws(b)) return true;
+            if (b == ':') { state = kJValue; return true; }
+            return false;
+        case kJArrValOrClose:
+            if (ws(b)) return true;
+            if (b == ']') {
+                if (depth == 0) return false;
+                depth -= 1;
+                state = depth == 0 ? kJFinished : kJCommaOrClose;
+                return true;
+            }
+            return value_start(b);
+        case kJValue:
+            if (ws(b)) return true;
+            return value_start(b);
+        case kJInStr:
+            return step_string(b, kJCommaOrClose);
+        case kJNum + kNumMinus:
+            if (b == '0') { state = kJNum + kNumZero; return true; }
+            if (b - '1' < 9u) { state = kJNum + kNumInt; return true; }
+            return false;
+        case kJNum + kNumZero:
+            if (b == '.') { state = kJNum + kNumDot; return true; }
+            if (b == 'e' || b == 'E') { state = kJNum + kNumExp; return true; }
+            return num_delim(b, kNumZero);
+        case kJNum + kNumInt:
+            if (digit(b)) return true;
+            if (b == '.') { state = kJNum + kNumDot; return true; }
+            if (b == 'e' || b == 'E') { state = kJNum + kNumExp; return true; }
+            return num_delim(b, kNumInt);
+        case kJNum + kNumDot:
+            if (digit(b)) { state = kJNum + kNumFrac; return true; }
+            return false;
+        case kJNum + kNumFrac:
+            if (digit(b)) return true;
+            if (b == 'e' || b == 'E') { state = kJNum + kNumExp; return true; }
+            return num_delim(b, kNumFrac);
+        case kJNum + kNumExp:
+            if (b == '+' || b == '-') { state = kJNum + kNumExpSign; return true; }
+            if (digit(b)) { state = kJNum + kNumExpDigits; return true; }
+            return false;
+        case kJNum + kNumExpSign:
+            if (digit(b)) { state = kJNum + kNumExpDigits; return true; }
+            return false;
+        case kJNum + kNumExpDigits:
+            if (digit(b)) return true;
+            return num_delim(b, kNumExpDigits);
+        case kJInLit:
+            if (lit_idx < lit_len && b == ((lit >> (8 * lit_idx)) & 0xFFu)) {
+                lit_idx += 1;
+                if (lit_idx == lit_len) state = kJCommaOrClose;
+                return true;
+            }
+            return false;
+        case kJCommaOrClose:
+            if (ws(b)) return true;
+            if (b == ',') return comma();
+            if (b == '}' || b == ']') return close(b);
+            return false;
+        case kJFinished:
+            return ws(b);
+        default:
+            return false;
+        }
+    }
+};
+
+// The state fields a piece can read, with the rest cleared: two states with
+// the same canonical form give the same mask.
+__host__ __device__ inline zi_json_state json_canonical(const zi_json_state &s) {
+    zi_json_state c{};
+    c.state = s.state;
+    c.depth = s.depth;
+    c.object_only = s.object_only;
+    c.stack = s.depth >= 64 ? s.stack : (s.stack & ((1ull << s.depth) - 1ull));
+    if (s.state == kJInKey || s.state == kJInStr) c.escape = s.escape;
+    if (s.state == kJInNum) c.num = s.num;
+    if (s.state == kJInLit) {
+        c.lit_len = s.lit_len;
+        c.lit_idx = s.lit_idx;
+        for (int i = 0; i < 8; ++i) c.lit_expected[i] = s.lit_expected[i];
+    }
+    return c;
+}
+
+}  // namespace zi

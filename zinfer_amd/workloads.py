@@ -10,6 +10,7 @@ window of 64 is exercised separately by the parity tests.
 from __future__ import annotations
 
 from dataclasses import dataclass, field
+from functools import lru_cache
 from typing import Optional
 
 import numpy as np
@@ -140,3 +141,82 @@ def pack_mask(bits: np.ndarray) -> np.ndarray:
 def mask_bit(mask: np.ndarray, ids: np.ndarray) -> np.ndarray:
     """Bit t of a packed row mask: (mask[t >> 5] >> (t & 31)) & 1."""
     return (mask[ids >> 5] >> (ids & 31).astype(np.uint32)) & 1
+
+
+# ------------------------------------------------------------ token pieces
+
+_JSON_FRAGMENTS = [
+    "{", "}", "[", "]", ":", ",", '"', '{"', '"}', '":', '": ', '": "', '",', '", "', '"},', '"}]', "},", "}]",
+    "],", "]}", "[{", '[{"', '["', '"]', ' {', ' [', ' "', '\n', '\n ', '\n  ', '\n    ', '\t', '\r\n', ' ', '  ',
+    '    ', 'true', 'false', 'null', ' true', ' false', ' null', 'tr', 'ue', 'fal', 'se', 'nu', 'll', 't', 'f',
+    'n', 'nul', 'fa', 'tru', '0', '1', '2', '9', '10', '12', '123', '2024', '-', '-1', '-0', '0.', '.', '.5', '.25',
+    'e', 'E', 'e+', 'e-', 'E+', '1e', '1e10', '3.14', '1.0', '00', '0x', '+1', '\\', '\\n', '\\"', '\\\\', '\\/',
+    '\\t', '\\u', '\\u00', '\\u12', '\\u12af', '\\ud83d', '\\q', '\\x', ': {', ': [', ', "', '": {', '": [',
+    '": true', '": null', '": 1', '":"', '","', '"],"', '},{"', 'NaN', 'Infinity', '1,', '1}', '1]', '0,', '0}',
+]
+_WORD_CHARS = "abcdefghijklmnopqrstuvwxyzABCDEFGHIJKLMNOPQRSTUVWXYZ0123456789_-./'"
+
+
+@lru_cache(maxsize=4)
+def synthetic_vocab(V: int = 151936, seed: int = 77):
+    """A seeded tokenizer vocabulary for the JSON mask: ids 0-255 are the single
+    bytes (control bytes and bytes >= 0x80 included), then JSON fragments, escapes,
+    numbers, literals, whitespace runs, word pieces with and without a leading
+    space, pieces longer than 12 bytes, a few empty pieces, and three
+    end-of-generation ids whose pieces are special-token text.
+
+    Returns (piece_off [V+1] u32, piece_buf u8, eog ids u32, eos id)."""
+    assert V >= 300
+    rng = np.random.Generator(np.random.PCG64(seed))
+    pieces: list = [bytes([b]) for b in range(256)]
+    pieces += [f.encode() for f in _JSON_FRAGMENTS]
+    specials = [b"<|endoftext|>", b"<|im_end|>", b"</s>"]
+    while len(pieces) < V:
+        u = rng.random()
+        if u < 0.50:  # word piece, often with a leading space
+            n = int(rng.integers(1, 11))
+            w = "".join(rng.choice(list(_WORD_CHARS[:52]), n))
+            pieces.append(((" " if rng.random() < 0.6 else "") + w).encode())
+        elif u < 0.62:  # digits / number fragments
+            n = int(rng.integers(1, 6))
+            w = "".join(rng.choice(list("0123456789"), n))
+            w = w + str(rng.choice(["", "", ".", ",", "}", "]", "e", "E+", " "]))
+            pieces.append(w.encode())
+        elif u < 0.74:  # JSON punctuation mixed with text
+            k = int(rng.integers(1, 4))
+            parts = [str(rng.choice(_JSON_FRAGMENTS)) for _ in range(k)]
+            pieces.append("".join(parts).encode())
+        elif u < 0.80:  # whitespace runs
+            n = int(rng.integers(1, 20))
+            pieces.append("".join(rng.choice([" ", " ", "\n", "\t", "\r"], n)).encode())
+        elif u < 0.86:  # long pieces (past the 12 inline bytes)
+            n = int(rng.integers(13, 90))
+            alphabet = list(_WORD_CHARS + ' "{}[]:,\\')
+            pieces.append("".join(rng.choice(alphabet, n)).encode())
+        elif u < 0.92:  # arbitrary bytes, including control bytes and UTF-8 tails
+            n = int(rng.integers(1, 8))
+            pieces.append(bytes(rng.integers(0, 256, n).astype(np.uint8).tolist()))
+        elif u < 0.9995:  # string content with escapes
+            n = int(rng.integers(1, 6))
+            parts = [str(rng.choice(["a", "b", " ", "\\n", "\\\"", "\\u00e9", "\\u12", "x", "\\\\", "é"]))
+                     for _ in range(n)]
+            pieces.append("".join(parts).encode())
+        else:
+            pieces.append(b"")
+    pieces = pieces[:V]
+    # end-of-generation ids: special-token text at fixed positions past the bytes
+    eog = np.array([V - 1, V // 2 + 1, 290], np.uint32)
+    for i, t in zip(eog.tolist(), specials):
+        pieces[i] = t
+    eos = int(eog[0])
+    lens = np.array([len(p) for p in pieces], np.int64)
+    off = np.zeros(V + 1, np.uint32)
+    off[1:] = np.cumsum(lens).astype(np.uint32)
+    buf = np.frombuffer(b"".join(pieces), dtype=np.uint8).copy()
+    for a in (off, buf, eog):
+        a.flags.writeable = False  # shared by the cache
+    return off, buf, eog, eos
+
+
+def vocab_piece(off: np.ndarray, buf: np.ndarray, i: int) -> bytes:
+    return bytes(buf[int(off[i]):int(off[i + 1])])
