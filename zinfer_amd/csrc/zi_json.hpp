@@ -250,4 +250,183 @@ __host__ __device__ inline zi_json_state json_canonical(const zi_json_state &s) 
     return c;
 }
 
+
+// ------------------------------------------------------------ table form
+// The finite part of the machine as one flat state (37 of them) and a
+// transition table over byte classes; the stack effects are six actions.
+// The table is derived from JsonFsm::step (json_build_tables) and checked
+// against it for every state, byte and stack shape before first use.
+enum : uint32_t {
+    kFStartObj, kFStartAny, kFKeyOrClose, kFKeyOnly, kFColon, kFValue, kFArrValOrClose, kFCommaOrClose,
+    kFFinished,
+    kFKey = 9,    // + EscapeState none..hex3
+    kFStr = 14,   // + EscapeState none..hex3
+    kFNum = 19,   // + NumState
+    kFLit = 27,   // true idx 1-3, false idx 1-4, null idx 1-3
+    kFCount = 37
+};
+enum : uint32_t { kAFail = 0x80, kAPushObj, kAPushArr, kAPop, kACloseObj, kACloseArr, kAComma };
+constexpr int kClsStride = 64;  // table row stride (byte classes per state <= 64)
+
+struct JsonTables {
+    uint8_t cls[256];                  // byte -> class
+    uint8_t tab[kFCount * kClsStride];  // flat state x class -> next flat state, or an action
+};
+
+constexpr uint64_t kLitTrue = 0x65757274ull, kLitFalse = 0x65736c6166ull, kLitNull = 0x6c6c756eull;
+
+// The flat state of a machine state, or -1 when it has none (a literal other
+// than true / false / null, or the unreachable hex4).
+__host__ __device__ inline int json_flat(const JsonFsm &f) {
+    switch (f.state) {
+    case kJStart: return f.object_only ? kFStartObj : kFStartAny;
+    case kJKeyOrClose: return kFKeyOrClose;
+    case kJKeyOnly: return kFKeyOnly;
+    case kJColon: return kFColon;
+    case kJValue: return kFValue;
+    case kJArrValOrClose: return kFArrValOrClose;
+    case kJCommaOrClose: return kFCommaOrClose;
+    case kJFinished: return kFFinished;
+    case kJInKey: return f.escape <= kEscHex3 ? (int)(kFKey + f.escape) : -1;
+    case kJInStr: return f.escape <= kEscHex3 ? (int)(kFStr + f.escape) : -1;
+    case kJInLit: {
+        const uint64_t m = f.lit_len >= 8 ? ~0ull : ((1ull << (8 * f.lit_len)) - 1ull);
+        const uint64_t w = f.lit & m;
+        if (f.lit_idx < 1 || f.lit_idx >= f.lit_len) return -1;
+        if (w == kLitTrue && f.lit_len == 4) return kFLit + f.lit_idx - 1;
+        if (w == kLitFalse && f.lit_len == 5) return kFLit + 3 + f.lit_idx - 1;
+        if (w == kLitNull && f.lit_len == 4) return kFLit + 7 + f.lit_idx - 1;
+        return -1;
+    }
+    default:
+        return f.state >= kJNum && f.state < kJNum + 8 ? (int)(kFNum + (f.state - kJNum)) : -1;
+    }
+}
+
+// A machine state for a flat state (escape / number / literal fields set).
+__host__ __device__ inline JsonFsm json_unflat(uint32_t fl, uint32_t depth, uint64_t stack) {
+    JsonFsm f{};
+    f.stack = stack;
+    f.depth = depth;
+    f.object_only = fl != kFStartAny;
+    f.num = kNumZero;
+    f.escape = kEscNone;
+    if (fl <= kFStartAny) f.state = kJStart;
+    else if (fl < kFKey) {
+        const uint32_t m[] = {kJStart, kJStart, kJKeyOrClose, kJKeyOnly, kJColon, kJValue, kJArrValOrClose,
+                              kJCommaOrClose, kJFinished};
+        f.state = m[fl];
+    } else if (fl < kFStr) { f.state = kJInKey; f.escape = fl - kFKey; }
+    else if (fl < kFNum) { f.state = kJInStr; f.escape = fl - kFStr; }
+    else if (fl < kFLit) { f.state = kJNum + (fl - kFNum); f.num = fl - kFNum; }
+    else {
+        const uint32_t k = fl - kFLit;
+        f.state = kJInLit;
+        if (k < 3) { f.lit = kLitTrue; f.lit_len = 4; f.lit_idx = k + 1; }
+        else if (k < 7) { f.lit = kLitFalse; f.lit_len = 5; f.lit_idx = k - 2; }
+        else { f.lit = kLitNull; f.lit_len = 4; f.lit_idx = k - 6; }
+    }
+    return f;
+}
+
+// One byte class through the table form.  fl / depth / stack are updated
+// only when the byte is accepted, as JsonFsm::step updates its fields.
+__host__ __device__ inline bool json_class_step(const uint8_t *tab, uint32_t &fl, uint32_t &depth, uint64_t &stack,
+                                                uint32_t c) {
+    const uint32_t e = tab[fl * kClsStride + c];
+    if (e < kAFail) {
+        fl = e;
+        return true;
+    }
+    if (e == kAFail) return false;
+    if (e == kAPushObj || e == kAPushArr) {
+        if (depth >= kJsonMaxDepth) return false;
+        const uint64_t bit = 1ull << depth;
+        stack = e == kAPushArr ? (stack | bit) : (stack & ~bit);
+        depth += 1;
+        fl = e == kAPushArr ? kFArrValOrClose : kFKeyOrClose;
+        return true;
+    }
+    if (depth == 0) return false;
+    const bool top_arr = (stack >> (depth - 1)) & 1ull;
+    if (e == kAComma) {
+        fl = top_arr ? kFValue : kFKeyOnly;
+        return true;
+    }
+    if ((e == kACloseObj && top_arr) || (e == kACloseArr && !top_arr)) return false;
+    depth -= 1;  // kAPop, or a close that matches the top
+    fl = depth == 0 ? kFFinished : kFCommaOrClose;
+    return true;
+}
+
+// The same step on a byte (class lookup first).
+__host__ __device__ inline bool json_table_step(const uint8_t *cls, const uint8_t *tab, uint32_t &fl,
+                                                uint32_t &depth, uint64_t &stack, uint32_t b) {
+    return json_class_step(tab, fl, depth, stack, cls[b]);
+}
+
+// Builds the table from JsonFsm::step and checks the table form against it
+// for every flat state, byte and stack shape.  Host only; false if they
+// disagree anywhere.
+inline bool json_build_tables(JsonTables &t) {
+    static uint8_t full[kFCount][256];
+    for (uint32_t fl = 0; fl < kFCount; ++fl)
+        for (uint32_t b = 0; b < 256; ++b) {
+            JsonFsm o = json_unflat(fl, 1, 0ull), a = json_unflat(fl, 1, 1ull);  // top .object / .array
+            const bool ok_o = o.step(b), ok_a = a.step(b);
+            uint32_t e;
+            if (!ok_o && !ok_a) e = kAFail;
+            else if (ok_o && ok_a && o.depth == 2 && a.depth == 2) e = ((o.stack >> 1) & 1ull) ? kAPushArr : kAPushObj;
+            else if (ok_o && ok_a && o.depth == 0 && a.depth == 0) e = kAPop;
+            else if (ok_o && !ok_a && o.depth == 0) e = kACloseObj;
+            else if (!ok_o && ok_a && a.depth == 0) e = kACloseArr;
+            else if (ok_o && ok_a && o.depth == 1 && a.depth == 1) {
+                const int fo = json_flat(o), fa = json_flat(a);
+                if (fo < 0 || fa < 0) return false;
+                if (fo == fa) e = (uint32_t)fo;
+                else if (fo == (int)kFKeyOnly && fa == (int)kFValue) e = kAComma;
+                else return false;
+            } else {
+                return false;
+            }
+            full[fl][b] = (uint8_t)e;
+        }
+    // byte classes: bytes with the same column share a class
+    int ncls = 0;
+    uint32_t rep[256];
+    for (uint32_t b = 0; b < 256; ++b) {
+        int c = -1;
+        for (int k = 0; k < ncls && c < 0; ++k) {
+            bool same = true;
+            for (uint32_t fl = 0; fl < kFCount && same; ++fl) same = full[fl][rep[k]] == full[fl][b];
+            if (same) c = k;
+        }
+        if (c < 0) {
+            if (ncls == kClsStride) return false;
+            rep[ncls] = b;
+            c = ncls++;
+        }
+        t.cls[b] = (uint8_t)c;
+    }
+    for (uint32_t fl = 0; fl < kFCount; ++fl)
+        for (int c = 0; c < kClsStride; ++c) t.tab[fl * kClsStride + c] = c < ncls ? full[fl][rep[c]] : (uint8_t)kAFail;
+    // check: table form == machine, every state x byte x stack shape
+    const uint32_t depths[] = {0, 1, 1, 2, 2, 63, 64, 64};
+    const uint64_t stacks[] = {0ull, 0ull, 1ull, 1ull, 2ull, 0x5555555555555555ull, ~0ull, 0ull};
+    for (uint32_t fl = 0; fl < kFCount; ++fl)
+        for (uint32_t b = 0; b < 256; ++b)
+            for (int s = 0; s < 8; ++s) {
+                JsonFsm m = json_unflat(fl, depths[s], stacks[s]);
+                const bool ok = m.step(b);
+                uint32_t f2 = fl, d2 = depths[s];
+                uint64_t s2 = stacks[s];
+                const bool ok2 = json_table_step(t.cls, t.tab, f2, d2, s2, b);
+                if (ok != ok2) return false;
+                if (!ok) continue;
+                const uint64_t mask = d2 >= 64 ? ~0ull : ((1ull << d2) - 1ull);
+                if ((int)f2 != json_flat(m) || d2 != m.depth || (s2 & mask) != (m.stack & mask)) return false;
+            }
+    return true;
+}
+
 }  // namespace zi
