@@ -33,6 +33,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=2048)
     ap.add_argument("--warmup", type=int, default=128)
     ap.add_argument("--config", type=int, default=2, help="BASELINE config to run (2 = headline)")
+    ap.add_argument("--path", choices=["sample", "json_mask"], default="sample",
+                    help="sample: zi_sample_rows on --config (the headline); json_mask: zi_json_mask_rows")
     ap.add_argument("--rotate-mib", type=int, default=512, help="distinct input bytes cycled through")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample (0 = skip)")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
@@ -68,6 +70,106 @@ def read_traffic(path: str, kernel: str, workload: str):
     return None
 
 
+def bench_json_mask(args):
+    """JSON grammar masks (zi_json_mask_rows, no state cache): 32 validator
+    states (seeded JSON prefixes) over a 151936-token synthetic vocabulary,
+    config 3's batch and vocabulary size.  One step = one call for the batch.
+    Every mask is checked against the oracle; the CPU baseline times the
+    oracle's applyMask restatement on the same states."""
+    import numpy as np
+    import torch
+
+    from zinfer_amd.api import Context, JsonValidator, Vocab
+    from zinfer_amd.workloads import json_prefixes, synthetic_vocab
+
+    V, rows = 151936, 32
+    off, buf, eog, eos = synthetic_vocab(V)
+    pre = json_prefixes(rows)
+    vals = []
+    for ob, text in pre:
+        v = JsonValidator(ob)
+        assert v.consume(text)
+        vals.append(v)
+    ctx = Context(0, max_rows=64, max_vocab=V)
+    vocab = Vocab(ctx, off, buf, eog, eos, cache_states=0)
+    W = (V + 31) // 32
+    dev = torch.device("cuda:0")
+    out = torch.empty((rows, W), dtype=torch.int32, device=dev)
+    inner = 16
+    stream = torch.cuda.Stream(dev)
+    with torch.cuda.stream(stream):
+        vocab.json_mask_rows(vals, out=out)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for _ in range(inner):
+                vocab.json_mask_rows(vals, out=out)
+        torch.cuda.synchronize()
+        reps = max(1, args.steps // inner)
+        for _ in range(max(1, args.warmup // inner)):
+            graph.replay()
+        torch.cuda.synchronize()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        ev0.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    steps = reps * inner
+    ms = ev0.elapsed_time(ev1) / steps
+    got = out.cpu().numpy().view(np.uint32)
+
+    from oracle import pyoracle
+
+    ostates = []
+    for ob, text in pre:
+        j = pyoracle.json_init(ob)
+        pyoracle.json_consume(j, text)
+        ostates.append(j)
+    t1, want = pyoracle.bench_json_mask(ostates, off, buf, eog, eos, 1)
+    parity = bool(np.array_equal(got, want))
+    cpu = None
+    if args.cpu_seconds > 0:
+        creps = max(1, int(args.cpu_seconds / max(t1, 1e-6)))
+        tc, _ = pyoracle.bench_json_mask(ostates, off, buf, eog, eos, creps)
+        cpu = {"value": round(rows * creps / tc, 1), "unit": "rows/s", "cores": 1, "kind": "port",
+               "sample": f"the same {rows} states x {creps} passes ({tc:.1f} s), oracle/grammar_oracle.c "
+                         f"(C restatement of src/grammar.zig:446-479), -O3, 1 thread"}
+    # bytes per call: per row the base mask read and the mask written (4 W each), the stack-token
+    # list pass reads each list token's class record, tail chunks and id once per row
+    # list tokens: pieces holding { } [ ] or , that are not end-of-generation ids (zi_vocab_create)
+    hit = np.isin(np.asarray(buf), np.frombuffer(b"{}[],", np.uint8))
+    cs = np.concatenate([[0], np.cumsum(hit)])
+    lens = np.diff(np.asarray(off)).astype(np.int64)
+    listed = (cs[np.asarray(off)[1:]] - cs[np.asarray(off)[:-1]]) > 0
+    listed[np.asarray(eog, dtype=np.int64)] = False
+    listed[eos] = False
+    S = int(listed.sum())
+    tail_bytes = int((16 * ((np.maximum(lens[listed] - 12, 0) + 15) // 16)).sum())
+    nbytes = rows * (8 * W + S * 20 + tail_bytes)
+    achieved = nbytes / (ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "JSON grammar mask rows/sec (zi_json_mask_rows, 151936-token vocabulary)",
+        "value": round(rows / (ms * 1e-3), 1), "unit": "rows/s", "n_gpus": 1, "steps": steps,
+        "warmup": max(1, args.warmup // inner) * inner, "ms_per_step": round(ms, 6), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "u8",
+        "data": "synthetic, seeded (zinfer_amd/workloads.py synthetic_vocab, json_prefixes)",
+        "config": {"workload": "json_mask_32x151936", "rows": rows, "vocab": V, "stack_tokens": S,
+                   "cache_states": 0, "launch": "hip_graph_replay", "parity_vs_oracle": parity},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": nbytes, "kernel": "json_list_kernel"},
+        "cpu_baseline": cpu,
+        "wall_s": round(wall, 3),
+    }), flush=True)
+    vocab.close()
+    ctx.close()
+    if not parity:
+        raise SystemExit("json_mask: GPU masks differ from the oracle")
+
+
 def main():
     args = parse()
     if args.copy_calibration:
@@ -79,6 +181,10 @@ def main():
               "multi-GPU sharding is described in DESIGN.md and not implemented). Use --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
+
+    if args.path == "json_mask":
+        bench_json_mask(args)
+        return
 
     import numpy as np
     import torch

@@ -220,3 +220,31 @@ def synthetic_vocab(V: int = 151936, seed: int = 77):
 
 def vocab_piece(off: np.ndarray, buf: np.ndarray, i: int) -> bytes:
     return bytes(buf[int(off[i]):int(off[i + 1])])
+
+
+def json_prefixes(n: int, seed: int = 606):
+    """Seeded JSON documents (json.dumps of random objects: strings with
+    escapes, numbers, literals, nested arrays and objects) cut at random
+    points: n pairs (object_only, prefix bytes), the validator states of a
+    JSON-mode decoding batch."""
+    import json
+    import random
+
+    r = random.Random(seed)
+    vals = [0, -17, 3.25, -1.5e-7, 12345678901, "", "plain text", 'q"uote', "back\\slash", "tab\there", "é€",
+            True, False, None]
+
+    def value(depth):
+        k = r.random()
+        if depth > 0 and k < 0.2:
+            return {"k%d" % i: value(depth - 1) for i in range(r.randint(0, 3))}
+        if depth > 0 and k < 0.35:
+            return [value(depth - 1) for _ in range(r.randint(0, 3))]
+        return r.choice(vals)
+
+    out = []
+    while len(out) < n:
+        obj = {"field_%d" % i: value(r.randint(0, 4)) for i in range(r.randint(1, 5))}
+        doc = json.dumps(obj, indent=r.choice([None, 2]), ensure_ascii=r.random() < 0.5).encode()
+        out.append((True, doc[: r.randint(0, len(doc) - 1)]))
+    return out
