@@ -162,3 +162,39 @@ def test_whole_vocab_large_batch(ctx, oracle, min_p, top_p):
     o = oracle_sample(oracle, pk, x, u, hist, hl)
     errs = compare_sample(g, o, pk, V, f"wl{min_p}")
     assert not errs, "\n".join(errs[:20])
+
+
+@pytest.mark.parametrize("seed,kind,pk_extra,bf16,use_mask", [
+    (1, "normal", dict(top_p=1.0, min_p=0.05), True, False),
+    (2, "normal", dict(top_p=0.9, min_p=0.3, temp=0.7), False, False),
+    (3, "t3", dict(top_p=0.98, min_p=0.02), True, True),
+    (4, "ints", dict(top_p=0.95, min_p=0.05), False, False),     # ties, -0.0 / +0.0
+    (5, "neginf", dict(top_p=0.98, min_p=0.05), True, False),    # mostly -inf rows
+    (6, "flat", dict(top_p=0.98, min_p=0.05), True, False),      # every entry ties the max: whole-order pass
+    (7, "normal", dict(top_p=0.98, min_p=0.9), True, False),     # often a single entry above the floor
+])
+def test_whole_vocab_large_batch_min_p_prefix(ctx, oracle, seed, kind, pk_extra, bf16, use_mask):
+    """>= 256 rows with min_p > 0: the prefix is every entry above a floor that
+    trails the row maximum (no top-256 selection); penalties that raise values
+    (repetition 0.9, negative presence) and rows the floor cannot settle."""
+    V, rows = 20000, 256
+    rng = np.random.Generator(np.random.PCG64(900 + seed))
+    x = _rows(rng, kind, rows, V)
+    if bf16:
+        x = _bf16_round(x)
+    u = rng.random((rows, 2), dtype=np.float32)
+    hist = rng.integers(0, V, (rows, 100), dtype=np.uint32)
+    hist[:, -6:] = np.argsort(-x, axis=1)[:, :6].astype(np.uint32)
+    hl = rng.integers(0, 101, rows).astype(np.int32)
+    pk = dict(temp=1.0, top_k=0, repeat_penalty=float(rng.choice([1.1, 0.9])), presence_penalty=-0.3,
+              penalty_last_n=100)
+    pk.update(pk_extra)
+    mask = None
+    if use_mask:
+        bits = rng.random((rows, (V + 31) // 32 * 32)) < 0.5
+        bits[:, 0] = True
+        mask = pack_mask(bits)
+    g = gpu_sample(ctx, pk, x, u, hist, hl, mask, bf16=bf16)
+    o = oracle_sample(oracle, pk, x, u, hist, hl, mask)
+    errs = compare_sample(g, o, pk, V, f"mp-{kind}")
+    assert not errs, "\n".join(errs[:20])

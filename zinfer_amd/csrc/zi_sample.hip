@@ -10,6 +10,8 @@
 // runs the reference tail on one wave: untempered top-p and min-p,
 // temperature weights, XTC and the draw, with every sum in the reference's
 // sequential f32 order.
+#include <type_traits>
+
 #include "zi_launch.hpp"
 #include "zi_rowpass.hpp"
 
@@ -66,9 +68,11 @@ __device__ __forceinline__ double chunk_stats_total(const SampleParams &P, int r
 }
 
 // tot: the row's total when the caller has it (>= 0), else taken from the
-// chunk records.
+// chunk records.  complete: every entry past the prefix fails min-p (the
+// prefix holds all entries above a threshold below mx + ln(min_p)), so the
+// min-p cut is at n at the latest.
 __device__ __forceinline__ bool nucleus_keep(const SampleParams &P, int row, const float *e, int n, int live,
-                                             int first_low, float mx, int &keep, double tot) {
+                                             int first_low, float mx, int &keep, double tot, bool complete) {
     int kp_lo = n + 1, kp_hi = n + 1;  // n + 1: past the prefix
     if (P.top_p < 1.0f) {
         if (!__builtin_isfinite(mx)) return false;
@@ -83,7 +87,8 @@ __device__ __forceinline__ bool nucleus_keep(const SampleParams &P, int row, con
         kp_lo = first_reach(e, live, P.top_p * lo, n + 1);
         kp_hi = first_reach(e, live, P.top_p * hi, n + 1);
     }
-    if (first_low < n && first_low < kp_lo) {  // min-p cuts before any possible keep (:229-234)
+    const bool cut = first_low < n || (complete && first_low == n);
+    if (cut && first_low < kp_lo) {  // min-p cuts before any possible keep (:229-234)
         keep = first_low > 1 ? first_low : 1;
         return true;
     }
@@ -102,7 +107,8 @@ __device__ __forceinline__ bool nucleus_keep(const SampleParams &P, int row, con
 // its flag, and the candidate outputs cover the kept entries.
 template <bool NUC>
 __device__ __forceinline__ void sample_tail(const SampleParams &P, int row, const uint64_t *okey, const float *oval,
-                                            int n, TailLds &tl, float u0, float u1, double tot = -1.0) {
+                                            int n, TailLds &tl, float u0, float u1, double tot = -1.0,
+                                            bool complete = false) {
     const int lane = threadIdx.x;
     float cv[4];
     uint32_t cid[4];
@@ -162,7 +168,7 @@ __device__ __forceinline__ void sample_tail(const SampleParams &P, int row, cons
     if (lane == 0) {
         int keep = n;
         if constexpr (NUC) {
-            settled0 = nucleus_keep(P, row, tl.e, n, live, first_low, mx, keep, tot) ? 1 : 0;
+            settled0 = nucleus_keep(P, row, tl.e, n, live, first_low, mx, keep, tot, complete) ? 1 : 0;
         } else {
             if (P.top_p < 1.0f) {  // :215-226
                 const float thr = P.top_p * lane_sum(tl.e, 0, live, 0.0f);
@@ -403,6 +409,16 @@ struct RowLoopLds {
     int32_t bn;
 };
 
+// The whole-vocabulary prefix threshold for min_p > 0: an entry below it has
+// exp(x - M) < min_p for every maximum >= M, with room for the f32 rounding of
+// x - M and of the threshold itself (rounded down).  Monotone in M.
+__device__ __forceinline__ float minp_floor(float M, double ln_minp) {
+    const double d = (double)M + ln_minp - 0.01 - 1e-6 * fabs((double)M);
+    float t = (float)d;
+    if ((double)t > d) t = __uint_as_float(t > 0.0f ? __float_as_uint(t) - 1u : __float_as_uint(t) + 1u);
+    return t;
+}
+
 // Entries of the sorted-descending list L[0, n) greater than `mine`.
 __device__ __forceinline__ int count_greater_n(const uint64_t *L, int n, uint64_t mine) {
     int lo = 0, hi = n;  // L[i] > mine for i < lo, L[i] <= mine for i >= hi
@@ -414,7 +430,7 @@ __device__ __forceinline__ int count_greater_n(const uint64_t *L, int n, uint64_
     return lo;
 }
 
-template <typename T, int NV, bool HAS_MASK, bool HAS_PEN, bool NUC>
+template <typename T, int NV, bool HAS_MASK, bool HAS_PEN, bool NUC, bool BY_MAX = false>
 __global__ __launch_bounds__(kThreads) void row_kernel(SampleParams P) {
     __shared__ union {
         SampleStageA<T, NV, HAS_PEN> a;
@@ -426,6 +442,7 @@ __global__ __launch_bounds__(kThreads) void row_kernel(SampleParams P) {
     __shared__ int s_dig[2];
     __shared__ int s_n;
     __shared__ float s_wmax[kWaves];
+    __shared__ float s_wmax2[kWaves];
     __shared__ double s_ws[kWaves];
 
     const RowSource &a = P.src;
@@ -441,13 +458,50 @@ __global__ __launch_bounds__(kThreads) void row_kernel(SampleParams P) {
     if constexpr (HAS_PEN) pen = &sm.a.p.pen;
     float ref = -INFINITY, S = 0.0f;  // NUC: running sum exp(x - ref) of this thread's elements
     int n_run = 0, cur = 0;           // running list length and buffer (uniform)
-    for (int g = 0; g < G; ++g) {
-        const int c0 = g * a.CH;
-        const int c1 = min(a.V, c0 + a.CH);
+    // NUC with min_p > 0: the prefix is every entry above minp_floor(row max)
+    // (the reference's keep never passes the first entry below min_p), so
+    // each chunk's threshold trails the running maximum of the unpenalized
+    // stream values instead of a top-256 selection.  It is also kept at or
+    // below the second largest lane maximum seen, which the row's second
+    // largest entry (the margin) is not below.
+    constexpr bool by_max = NUC && BY_MAX;  // launched only when min_p > 0
+    const double ln_minp = by_max ? log((double)P.min_p) : 0.0;
+    float m_run = -INFINITY, m2_run = -INFINITY;  // two largest lane maxima so far (distinct lanes)
+    // The row in steps of what the registers hold (the plan's chunking only
+    // sets the layout of the row-total record below).
+    constexpr int SUB = kThreads * NV * VecTraits<T>::VEC;
+    for (int c0 = 0; c0 < a.V; c0 += SUB) {
+        const int c1 = min(a.V, c0 + SUB);
         PenOwn own;
         ChunkRegs<T, NV> cr;
         chunk_stream<T, NV, HAS_MASK, HAS_PEN>(a, row, c0, c1, cr, pen, &own);
-        float tau = select_prepare<T, NV>(cr.lmax, k, sm.a.sel, s_tau, &s_n);
+        float tau;
+        if constexpr (by_max) {
+            const float lm = cr.lmax;
+            const float wm = wave_max_f(lm);
+            const uint64_t top = ballot(lm == wm);
+            const float w2 = __popcll(top) >= 2 ? wm : wave_max_f(lm == wm ? -INFINITY : lm);
+            if (lane == 0) {
+                s_wmax[wid] = wm;
+                s_wmax2[wid] = w2;
+            }
+            if (tid == 0) s_n = 0;
+            if (tid < kSortMax) sm.a.sel.rank[tid] = 0u;
+            __syncthreads();
+#pragma unroll
+            for (int w = 0; w < 2 * kWaves; ++w) {
+                const float v = w < kWaves ? s_wmax[w] : s_wmax2[w - kWaves];
+                if (v > m_run) {
+                    m2_run = m_run;
+                    m_run = v;
+                } else if (v > m2_run) {
+                    m2_run = v;
+                }
+            }
+            tau = m_run == -INFINITY ? -INFINITY : fminf(minp_floor(m_run, ln_minp), m2_run);
+        } else {
+            tau = select_prepare<T, NV>(cr.lmax, k, sm.a.sel, s_tau, &s_n);
+        }
         if (n_run == k) tau = fmaxf(tau, okey_inv((uint32_t)(rl.key[cur][k - 1] >> 32)));
         chunk_select_publish<T, NV, HAS_PEN, true>(a, cr, c0, k, sm.a.sel, pen, &own, s_tau, &s_n, s_bins, s_dig,
                                                    ChunkOut{rl.bk, rl.bv, &rl.bn}, tau);
@@ -515,6 +569,14 @@ __global__ __launch_bounds__(kThreads) void row_kernel(SampleParams P) {
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) Z += s_ws[w];
         tot = (n_run > 0) ? Z * exp((double)M - (double)rl.val[cur][0]) : 0.0;
+        // the row total as the plan's per-chunk (max, sum) records, which the
+        // whole-order pass reads for its bounds: all of it in record 0
+        if (tid < G) {
+            double *gs = P.g_stat + ((int64_t)row * G + tid) * 3;
+            gs[0] = tid == 0 ? (double)M : -INFINITY;
+            gs[1] = tid == 0 ? Z : 0.0;
+            gs[2] = 0.0;
+        }
     }
     if (tid >= 64) return;  // the tail runs on wave 0 with all 64 lanes active
     if (n_run == 0) {
@@ -530,13 +592,37 @@ __global__ __launch_bounds__(kThreads) void row_kernel(SampleParams P) {
         }
         return;
     }
-    sample_tail<NUC>(P, row, rl.key[cur], rl.val[cur], n_run, sm.tl, u0, u1, tot);
+    int n = n_run;
+    bool complete = false;
+    if constexpr (by_max) {  // trim to the final threshold: the list is then a prefix of the row's order
+        const float mx = rl.val[cur][0];
+        const float tf = minp_floor(mx, ln_minp);
+        int m = 0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int i = lane + 64 * c;
+            m += __popcll(ballot(i < n_run && rl.val[cur][i] >= tf));
+        }
+        n = (mx == mx && mx != -INFINITY) ? max(m, min(2, n_run)) : n_run;  // the top two are exact
+        complete = m < k && mx == mx && mx != -INFINITY;  // nothing above tf was dropped by the cap
+        if (n < 2 && P.n_all >= 2) {  // fewer than two entries in the row: whole-order pass
+            if (tid == 0) P.nuc_flag[row] = 1;
+            return;
+        }
+    }
+    sample_tail<NUC>(P, row, rl.key[cur], rl.val[cur], n, sm.tl, u0, u1, tot, complete);
 }
 
 template <bool NUC, typename T, int NV, bool M, bool PN>
 static hipError_t launch_sample_t(const SampleParams &P, int rows, hipStream_t st) {
     if (rows >= kRowLoopRows) {  // one workgroup per row fills the device
-        hipLaunchKernelGGL((row_kernel<T, NV, M, PN, NUC>), dim3(rows), dim3(kThreads), 0, st, P);
+        // min_p > 0 prefix: 32 elements per thread per step (the 64-element
+        // instances of this variant run out of registers)
+        constexpr int NVM = std::is_same<T, float>::value ? 8 : 4;
+        if (NUC && P.min_p > 0.0f)
+            hipLaunchKernelGGL((row_kernel<T, NVM, M, PN, true, true>), dim3(rows), dim3(kThreads), 0, st, P);
+        else
+            hipLaunchKernelGGL((row_kernel<T, NV, M, PN, NUC>), dim3(rows), dim3(kThreads), 0, st, P);
         return hipGetLastError();
     }
     dim3 grid(rows * P.src.G), block(kThreads);
