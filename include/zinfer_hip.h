@@ -75,6 +75,7 @@ void zi_params_default(zi_params *p);
 /* ---------------------------------------------------------------- context */
 
 typedef struct zi_ctx zi_ctx;
+typedef struct zi_vocab zi_vocab; /* token pieces on the device (JSON grammar masks, below) */
 
 /* Creates a context on HIP device `device` able to serve batches of up to
  * max_rows rows of up to max_vocab logits.  It owns a HIP stream (default
@@ -203,7 +204,6 @@ int32_t zi_json_try_consume(const zi_json_state *s, const uint8_t *piece, size_t
  * every reference call site passes to applyMask (g.tok.eos, src/gen.zig:458;
  * -1 for none).  Host arrays, copied (synchronous).  cache_states > 0 keeps
  * that many per-state masks on the device (least recently used replaced). */
-typedef struct zi_vocab zi_vocab;
 int32_t zi_vocab_create(zi_vocab **out, zi_ctx *ctx, const uint32_t *piece_off, const uint8_t *piece_buf,
                         uint32_t n_vocab, const uint32_t *eog, uint32_t n_eog, int64_t eos,
                         int32_t cache_states);
@@ -242,6 +242,23 @@ void    zi_sampler_apply_dry(const zi_sampler *s, float *logits, uint32_t n);
 int32_t zi_sampler_sample_with_margin(zi_sampler *s, float *logits, uint32_t n, uint32_t *tok,
                                       float *margin);
 int32_t zi_sampler_sample(zi_sampler *s, float *logits, uint32_t n, uint32_t *tok); /* :279 */
+/* Draft verification (src/gen.zig:544-587) in one batched launch.  Row i of
+ * b (device logits, i = 0..k) is the target's output after cur_tok and
+ * draft[0..i); it is sampled with the state the reference would have after
+ * take(draft[0..i)): penalty window and DRY history with the prefix appended,
+ * JSON validator (when v and json are given) after consuming its pieces, and
+ * the RNG draws of rows 0..i-1 spent.  Acceptance stops at the first row whose
+ * token differs from the draft, is in eog, or once max_accept tokens are taken;
+ * with all k accepted, row k (the bonus row) gives the next token.  Returns the
+ * accepted count, the next token and its margin, and leaves the sampler (and
+ * *json) as the reference leaves them: draft[0..accepted) accepted (pieces
+ * consumed), the RNG advanced by the draws of the rows it sampled.  The next
+ * token is not accepted.  k <= 16; only logits, dtype, rows (>= k + 1), vocab
+ * and ld of b are read.  Synchronous. */
+int32_t zi_sampler_verify(zi_sampler *s, const zi_batch *b, const uint32_t *draft, uint32_t k,
+                          uint32_t max_accept, const uint32_t *eog, uint32_t n_eog, zi_vocab *v,
+                          zi_json_state *json, uint32_t *out_accepted, uint32_t *out_next,
+                          float *out_margin);
 /* Read / replace the params (server.zig:377-415 writes g.smp.p fields). */
 void    zi_sampler_get_params(const zi_sampler *s, zi_params *p);
 void    zi_sampler_set_params(zi_sampler *s, const zi_params *p);

@@ -200,6 +200,23 @@ class Sampler:
     def sample(self, logits) -> int:
         return self.sample_with_margin(logits)[0]
 
+    def verify(self, logits: torch.Tensor, draft, *, max_accept: int = 2**32 - 1, eog=(), vocab=None,
+               json: Optional["JsonValidator"] = None):
+        """Draft verification in one batched launch (zi_sampler_verify, src/gen.zig:544-587).
+        logits: device [>= len(draft) + 1][V].  Returns (accepted, next_tok, margin)."""
+        import numpy as np
+        d = np.ascontiguousarray(np.asarray(draft, dtype=np.uint32).reshape(-1))
+        e = np.ascontiguousarray(np.asarray(eog, dtype=np.uint32).reshape(-1))
+        b = Context.batch(logits, self.vocab)
+        a, nt, m = C.c_uint32(), C.c_uint32(), C.c_float()
+        self.ctx._bind_stream()
+        check(lib().zi_sampler_verify(self.h, C.byref(b), d.ctypes.data_as(_lib.u32p) if d.size else None, d.size,
+                                      max_accept, e.ctypes.data_as(_lib.u32p) if e.size else None, e.size,
+                                      vocab.h if vocab is not None else None,
+                                      C.byref(json.st) if json is not None else None,
+                                      C.byref(a), C.byref(nt), C.byref(m)))
+        return int(a.value), int(nt.value), float(m.value)
+
     def get_params(self) -> ZiParams:
         p = ZiParams()
         lib().zi_sampler_get_params(self.h, C.byref(p))

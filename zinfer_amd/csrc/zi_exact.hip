@@ -540,7 +540,7 @@ __global__ __launch_bounds__(kThreads) void exact_kernel(ExactParams P) {
             if (tid == 0) {
                 const int fl = first >= 0 ? first : m;  // <= m
                 if (P.top_p >= 1.0f) res = fl < n ? max(fl, 1) : n;
-                else if (ok_bounds && fl < kp_lo) res = max(fl, 1);
+                else if (ok_bounds && fl <= kp_lo) res = max(fl, 1);  // keep = min(keep_p, fl)
                 else if (ok_bounds && kp_lo == kp_hi && kp_lo <= m) res = kp_lo;
                 s_i[0] = res;
             }

@@ -233,7 +233,18 @@ struct zi_vocab {
     std::vector<uint64_t> used;  // last call that used the slot (0: empty)
     uint64_t calls = 0;
     std::vector<uint32_t> host_mask;
+    std::vector<uint32_t> h_off;  // host copy of the pieces (for host-side consume)
+    std::vector<uint8_t> h_buf;
 };
+
+int32_t zi_vocab_size(const zi_vocab *v) { return v ? v->V : 0; }
+
+bool zi_vocab_piece(const zi_vocab *v, uint32_t id, const uint8_t **p, uint32_t *n) {
+    if (!v || id >= (uint32_t)v->V) return false;
+    *p = v->h_buf.data() + v->h_off[id];
+    *n = v->h_off[id + 1] - v->h_off[id];
+    return true;
+}
 
 static void release(zi_vocab *v) {
     if (!v) return;
@@ -604,6 +615,8 @@ int32_t zi_vocab_create(zi_vocab **out, zi_ctx *ctx, const uint32_t *piece_off, 
     }
     v->key.resize(v->cap);
     v->used.assign(v->cap, 0);
+    v->h_off.assign(piece_off, piece_off + V + 1);
+    v->h_buf.assign(piece_buf, piece_buf + nbuf);
     *out = v;
     return ZI_OK;
 }

@@ -177,6 +177,7 @@ struct zi_sampler {
     uint32_t breakers[kMaxBreakers];
     uint32_t n_breakers = 0;
     Staging st;
+    Staging vst;  // zi_sampler_verify, allocated on first use
     // staging layout (bytes)
     size_t o_logits = 0, o_hist = 0, o_hlen = 0, o_eids = 0, o_edel = 0, o_ecnt = 0, o_u = 0, o_tok = 0,
            o_margin = 0, o_ndraws = 0, total = 0;
@@ -339,6 +340,176 @@ extern "C" int32_t zi_sampler_sample_with_margin(zi_sampler *s, float *logits, u
         if (eids[i] < n) logits[eids[i]] -= edel[i];
     *tok = *(uint32_t *)(h + s->o_tok);
     if (margin) *margin = *(float *)(h + s->o_margin);
+    return ZI_OK;
+}
+
+// ------------------------------------------------ batched draft verification
+// src/gen.zig:544-587 verifies a draft row by row: row i is sampled with the
+// state after take(draft[0..i)) (penalty ring, DRY history, JSON validator)
+// and the next draws of the RNG, and acceptance stops at the first row whose
+// token differs from the draft (or is end-of-generation); with every draft
+// token accepted, row k (the bonus row) gives the next token.  Every row's
+// state is known up front, so all k + 1 rows go in one zi_sample_rows launch;
+// only the draws need care: a row takes 0 (greedy), 1, or 2 (XTC chance)
+// uniforms, decided by its data and not by the uniform values, so when XTC can
+// fire a first launch finds each row's count and a second one runs with each
+// row's uniforms at its offset in the stream.
+constexpr uint32_t kMaxVerify = 16;  // drafted tokens per call (the reference drafts at most 8)
+
+extern "C" int32_t zi_sampler_verify(zi_sampler *s, const zi_batch *b, const uint32_t *draft, uint32_t k,
+                                     uint32_t max_accept, const uint32_t *eog, uint32_t n_eog, zi_vocab *v,
+                                     zi_json_state *json, uint32_t *out_accepted, uint32_t *out_next,
+                                     float *out_margin) {
+    if (!s || !b || !b->logits || (k && !draft) || (n_eog && !eog) || !out_accepted || !out_next)
+        return zi_fail(ZI_ERR_INVALID, "zi_sampler_verify: bad argument");
+    if (k > kMaxVerify) return zi_fail(ZI_ERR_UNSUPPORTED, "zi_sampler_verify: k=%u > %u", k, kMaxVerify);
+    if ((uint32_t)b->vocab != s->vocab || b->rows < (int32_t)k + 1)
+        return zi_fail(ZI_ERR_INVALID, "zi_sampler_verify: batch of %d x %d for k=%u, vocab %u", b->rows, b->vocab, k,
+                       s->vocab);
+    if ((v == nullptr) != (json == nullptr))
+        return zi_fail(ZI_ERR_INVALID, "zi_sampler_verify: vocab and json state go together");
+    if (v && zi_vocab_size(v) != (int32_t)s->vocab)
+        return zi_fail(ZI_ERR_INVALID, "zi_sampler_verify: vocab has %d tokens, sampler %u", zi_vocab_size(v), s->vocab);
+    zi_ctx *c = s->ctx;
+    const uint32_t R = k + 1;
+    if ((int32_t)R > c->max_rows) return zi_fail(ZI_ERR_CAPACITY, "zi_sampler_verify: %u rows > max_rows", R);
+    const zi_params &p = s->p;
+    if (p.penalty_last_n > (uint32_t)zi::kMaxWinHost)
+        return zi_fail(ZI_ERR_UNSUPPORTED, "penalty_last_n %u > %d", p.penalty_last_n, zi::kMaxWinHost);
+    const uint32_t W = (s->vocab + 31) / 32;
+    const uint32_t RM = kMaxVerify + 1;
+    size_t o = 0;
+    const size_t o_hist = o;
+    o = align_up(o + (size_t)RM * zi::kMaxWinHost * 4, 256);
+    const size_t o_hlen = o;
+    o = align_up(o + RM * 4, 256);
+    const size_t o_eids = o;
+    o = align_up(o + (size_t)RM * zi::kMaxEditsHost * 4, 256);
+    const size_t o_edel = o;
+    o = align_up(o + (size_t)RM * zi::kMaxEditsHost * 4, 256);
+    const size_t o_ecnt = o;
+    o = align_up(o + RM * 4, 256);
+    const size_t o_u = o;
+    o = align_up(o + RM * 8, 256);
+    const size_t o_in = o;  // host -> device up to here
+    const size_t o_tok = o;
+    o = align_up(o + RM * 4, 256);
+    const size_t o_margin = o;
+    o = align_up(o + RM * 4, 256);
+    const size_t o_nd = o;
+    o = align_up(o + RM * 4, 256);
+    const size_t o_out = o;  // device -> host from o_tok to here
+    const size_t o_mask = o;
+    o = align_up(o + (size_t)RM * W * 4, 256);
+    hipError_t e = hipSetDevice(c->device);
+    if (e != hipSuccess) return zi_hip_fail(e, "zi_sampler_verify: hipSetDevice");
+    int32_t rc = s->vst.ensure(o);
+    if (rc) return rc;
+    char *h = (char *)s->vst.h;
+    char *d = (char *)s->vst.d;
+
+    // per-row penalty windows and DRY edits: the history plus draft[0..i)
+    uint32_t lin[kMaxHistory + kMaxVerify];
+    const uint32_t nlin = s->window(kMaxHistory, lin);
+    std::memcpy(lin + nlin, draft, (size_t)k * 4);
+    bool any_edits = false;
+    for (uint32_t i = 0; i < R; ++i) {
+        const uint32_t len = nlin + i;
+        const uint32_t nw = std::min<uint32_t>(len, p.penalty_last_n);
+        std::memcpy(h + o_hist + (size_t)i * zi::kMaxWinHost * 4, lin + len - nw, (size_t)nw * 4);
+        ((int32_t *)(h + o_hlen))[i] = (int32_t)nw;
+        uint32_t ne = 0;
+        if (p.dry_multiplier != 0.0f) {
+            const uint32_t hl = std::min<uint32_t>(len, kMaxHistory);
+            ne = zi_dry_edits_impl(lin + len - hl, hl, s->breakers, s->n_breakers, p,
+                                   (uint32_t *)(h + o_eids) + (size_t)i * zi::kMaxEditsHost,
+                                   (float *)(h + o_edel) + (size_t)i * zi::kMaxEditsHost);
+        }
+        ((int32_t *)(h + o_ecnt))[i] = (int32_t)ne;
+        any_edits |= ne > 0;
+    }
+    // per-row JSON states: the validator after consuming draft[0..i)
+    zi_json_state states[kMaxVerify + 1];
+    if (v) {
+        zi_json_state st = *json;
+        for (uint32_t i = 0; i < R; ++i) {
+            states[i] = st;
+            if (i < k) {
+                const uint8_t *pc;
+                uint32_t pn;
+                if (!zi_vocab_piece(v, draft[i], &pc, &pn))
+                    return zi_fail(ZI_ERR_INVALID, "zi_sampler_verify: draft token %u out of range", draft[i]);
+                zi_json_consume(&st, pc, pn);
+            }
+        }
+    }
+    // draws: row i takes its uniforms at offset off[i] of the stream
+    Xoshiro peek = s->rng;
+    float stream[2 * (kMaxVerify + 1) + 2];
+    for (uint32_t i = 0; i < 2 * R + 2; ++i) stream[i] = peek.f32();
+    const bool sampled = p.temp > 0.0f;
+    const bool xtc = sampled && p.xtc_probability > 0.0f && p.xtc_threshold <= 0.5f;
+    int32_t nd[kMaxVerify + 1];
+    for (uint32_t i = 0; i < R; ++i) nd[i] = sampled ? 1 : 0;
+
+    zi_batch bb = *b;
+    bb.rows = (int32_t)R;
+    bb.hist = (const uint32_t *)(d + o_hist);
+    bb.hist_len = (const int32_t *)(d + o_hlen);
+    bb.hist_ld = zi::kMaxWinHost;
+    bb.mask = v ? (const uint32_t *)(d + o_mask) : nullptr;
+    bb.mask_ld = (int32_t)W;
+    bb.edit_ids = any_edits ? (const uint32_t *)(d + o_eids) : nullptr;
+    bb.edit_delta = any_edits ? (const float *)(d + o_edel) : nullptr;
+    bb.edit_count = any_edits ? (const int32_t *)(d + o_ecnt) : nullptr;
+    bb.edit_ld = zi::kMaxEditsHost;
+    zi_sample_out so;
+    std::memset(&so, 0, sizeof so);
+    so.tok = (uint32_t *)(d + o_tok);
+    so.margin = (float *)(d + o_margin);
+    so.ndraws = (int32_t *)(d + o_nd);
+    if (v) {
+        rc = zi_json_mask_rows(c, v, states, (int32_t)R, (uint32_t *)(d + o_mask), (int32_t)W);
+        if (rc) return rc;
+    }
+    for (int pass = xtc ? 0 : 1; pass < 2; ++pass) {
+        float *u = (float *)(h + o_u);
+        uint32_t off = 0;
+        for (uint32_t i = 0; i < R; ++i) {
+            u[2 * i] = stream[off];
+            u[2 * i + 1] = stream[off + 1];
+            off += (uint32_t)nd[i];
+        }
+        e = hipMemcpyAsync(d, h, o_in, hipMemcpyHostToDevice, c->stream);
+        if (e != hipSuccess) return zi_hip_fail(e, "zi_sampler_verify: H2D");
+        rc = zi_sample_rows(c, &p, &bb, (const float *)(d + o_u), &so);
+        if (rc) return rc;
+        e = hipMemcpyAsync(h + o_tok, d + o_tok, o_out - o_tok, hipMemcpyDeviceToHost, c->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+        if (e != hipSuccess) return zi_hip_fail(e, "zi_sampler_verify: D2H");
+        for (uint32_t i = 0; i < R; ++i) nd[i] = ((const int32_t *)(h + o_nd))[i];
+    }
+    const uint32_t *tok = (const uint32_t *)(h + o_tok);
+    const float *mg = (const float *)(h + o_margin);
+    uint32_t a = 0;
+    while (a < k && a < max_accept && tok[a] == draft[a] && std::find(eog, eog + n_eog, tok[a]) == eog + n_eog) ++a;
+    // side effects of the reference loop: take() for the accepted tokens, and
+    // the draws of rows 0..a (the rows it sampled)
+    uint32_t used = 0;
+    for (uint32_t i = 0; i <= a; ++i) used += (uint32_t)nd[i];
+    for (uint32_t i = 0; i < used; ++i) (void)s->rng.f32();
+    for (uint32_t i = 0; i < a; ++i) {
+        zi_sampler_accept(s, draft[i]);
+        if (v) {
+            const uint8_t *pc;
+            uint32_t pn;
+            zi_vocab_piece(v, draft[i], &pc, &pn);
+            zi_json_consume(json, pc, pn);
+        }
+    }
+    *out_accepted = a;
+    *out_next = tok[a];
+    if (out_margin) *out_margin = mg[a];
     return ZI_OK;
 }
 

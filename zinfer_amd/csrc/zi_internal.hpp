@@ -31,3 +31,8 @@ struct zi_ctx {
 
 int32_t zi_fail(int32_t code, const char *fmt, ...);
 int32_t zi_hip_fail(hipError_t e, const char *what);
+
+// Internal view of a zi_vocab (zi_grammar.hip) for the host drivers: its
+// size, and a token's piece bytes (host copy).
+int32_t zi_vocab_size(const zi_vocab *v);
+bool zi_vocab_piece(const zi_vocab *v, uint32_t id, const uint8_t **p, uint32_t *n);

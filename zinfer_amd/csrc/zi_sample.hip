@@ -87,8 +87,11 @@ __device__ __forceinline__ bool nucleus_keep(const SampleParams &P, int row, con
         kp_lo = first_reach(e, live, P.top_p * lo, n + 1);
         kp_hi = first_reach(e, live, P.top_p * hi, n + 1);
     }
+    // The reference's keep is min(keep_p, first_low) (first_low >= 1: the
+    // maximum's term is 1): min-p cuts at first_low unless keep_p comes first,
+    // and when keep_p == first_low the two agree.
     const bool cut = first_low < n || (complete && first_low == n);
-    if (cut && first_low < kp_lo) {  // min-p cuts before any possible keep (:229-234)
+    if (cut && first_low <= kp_lo) {  // min-p decides keep (:229-234)
         keep = first_low > 1 ? first_low : 1;
         return true;
     }
