@@ -33,8 +33,9 @@ def parse():
     ap.add_argument("--steps", type=int, default=2048)
     ap.add_argument("--warmup", type=int, default=128)
     ap.add_argument("--config", type=int, default=2, help="BASELINE config to run (2 = headline)")
-    ap.add_argument("--path", choices=["sample", "json_mask"], default="sample",
-                    help="sample: zi_sample_rows on --config (the headline); json_mask: zi_json_mask_rows")
+    ap.add_argument("--path", choices=["sample", "json_mask", "verify"], default="sample",
+                    help="sample: zi_sample_rows on --config (the headline); json_mask: zi_json_mask_rows; "
+                         "verify: zi_sampler_verify")
     ap.add_argument("--rotate-mib", type=int, default=512, help="distinct input bytes cycled through")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample (0 = skip)")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
@@ -170,6 +171,94 @@ def bench_json_mask(args):
         raise SystemExit("json_mask: GPU masks differ from the oracle")
 
 
+def bench_verify(args):
+    """Draft verification (zi_sampler_verify, src/gen.zig:544-587): 8 drafted
+    tokens + the bonus row over a 151936-token f32 vocabulary, device logits.
+    One step = one verify call (synchronous: the accepted count comes back to
+    the host).  For contrast the same rows are also sampled one call per row
+    through the host-row Sampler (the reference API shape: host logits in).
+    The CPU baseline is the oracle's sequential verify loop."""
+    import numpy as np
+    import torch
+
+    from zinfer_amd.api import Context, Sampler, params
+
+    V, k = 151936, 8
+    rng = np.random.Generator(np.random.PCG64(808))
+    X = (rng.standard_normal((k + 1, V)) * 2.5).astype(np.float32)
+    draft = [int(t) for t in rng.integers(0, V, k)]
+    for i, t in enumerate(draft):
+        X[i, t] += 25.0  # the target agrees with the draft (well above the row maximum)
+    pk = dict(temp=0.8, top_k=40, top_p=0.95, min_p=0.05, repeat_penalty=1.1, penalty_last_n=64, seed=9)
+    hist = [int(t) for t in rng.integers(0, V, 64)]
+    ctx = Context(0, max_rows=16, max_vocab=V)
+    dev = torch.device("cuda:0")
+    L = torch.from_numpy(X).to(dev)
+    smp = Sampler(ctx, V, params(**pk))
+    for t in hist:
+        smp.accept(t)
+    for _ in range(max(1, args.warmup // 16)):
+        smp.verify(L, draft)
+    torch.cuda.synchronize()
+    steps = max(16, args.steps)
+    accepted = []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        accepted.append(smp.verify(L, draft)[0])
+    wall = time.perf_counter() - t0
+    ms = wall * 1e3 / steps
+    # one call per row through the host-row sampler, for contrast
+    seq = Sampler(ctx, V, params(**pk))
+    for t in hist:
+        seq.accept(t)
+    reps = max(4, steps // 8)
+    t1 = time.perf_counter()
+    for _ in range(reps):
+        for i in range(k + 1):
+            seq.sample_with_margin(X[i].copy())
+    ms_seq = (time.perf_counter() - t1) * 1e3 / reps
+
+    from oracle import pyoracle
+
+    op = pyoracle.params(**{kk: v for kk, v in pk.items() if kk != "seed"})
+    stream = pyoracle.rng_floats(9, 64)
+    cpu = None
+    if args.cpu_seconds > 0:
+        n_cpu, tc0 = 0, time.perf_counter()
+        while time.perf_counter() - tc0 < min(args.cpu_seconds, 10.0):
+            h, pos = list(hist), 0
+            for i in range(k + 1):
+                tok, _, d = pyoracle.sample_row(op, X[i], stream[pos:pos + 2], window=np.array(h[-64:], np.uint32))
+                pos += d["ndraws"]
+                if i < k and tok == draft[i]:
+                    h.append(tok)
+                    continue
+                break
+            n_cpu += 1
+        tc = time.perf_counter() - tc0
+        cpu = {"value": round(n_cpu / tc, 2), "unit": "verify calls/s", "cores": 1, "kind": "port",
+               "sample": f"{n_cpu} sequential verify loops of {k} drafted tokens + bonus row ({tc:.1f} s), "
+                         f"oracle/oracle.c sample_row (C restatement of src/sampler.zig:190-276), 1 thread"}
+    nbytes = (k + 1) * V * 4
+    achieved = nbytes / (ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "draft verification calls/sec (zi_sampler_verify, 8 drafted tokens + bonus row, V=151936 f32)",
+        "value": round(1e3 / ms, 1), "unit": "verify calls/s", "n_gpus": 1, "steps": steps,
+        "warmup": max(1, args.warmup // 16), "ms_per_step": round(ms, 6), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic, seeded (bench.py bench_verify): N(0, 2.5^2) rows, draft tokens +25",
+        "config": {"workload": "verify_k8_151936_f32", "drafted": k, "vocab": V, **pk,
+                   "accepted_mean": float(np.mean(accepted)), "one_call_per_row_ms": round(ms_seq, 4),
+                   "timing": "host wall clock per synchronous call"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": nbytes, "kernel": "sample_kernel"},
+        "cpu_baseline": cpu,
+        "wall_s": round(wall, 3),
+    }), flush=True)
+    ctx.close()
+
+
 def main():
     args = parse()
     if args.copy_calibration:
@@ -184,6 +273,9 @@ def main():
 
     if args.path == "json_mask":
         bench_json_mask(args)
+        return
+    if args.path == "verify":
+        bench_verify(args)
         return
 
     import numpy as np
