@@ -36,6 +36,8 @@ def parse():
     ap.add_argument("--path", choices=["sample", "json_mask", "verify"], default="sample",
                     help="sample: zi_sample_rows on --config (the headline); json_mask: zi_json_mask_rows; "
                          "verify: zi_sampler_verify")
+    ap.add_argument("--softcap", type=float, default=0.0,
+                    help="final-logit softcap fused into the read (sample path; 0 = off, the config's default)")
     ap.add_argument("--rotate-mib", type=int, default=512, help="distinct input bytes cycled through")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample (0 = skip)")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
@@ -367,6 +369,8 @@ def main():
     dev = torch.device("cuda:0")
     w = CONFIGS[args.config]()
     rows, V = w.rows, w.vocab
+    if args.softcap > 0:
+        w.params = dict(w.params, final_logit_softcap=args.softcap)
     if args.config == 4:
         bench_entropy(args, w)
         return

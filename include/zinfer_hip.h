@@ -67,6 +67,10 @@ typedef struct zi_params {
     float    xtc_threshold;      /* 0.1 */
     uint32_t xtc_min_keep;       /* 1 */
     uint64_t seed;               /* 0    (host Sampler RNG seed) */
+    float    final_logit_softcap; /* 0   (0 = off) cap*tanh(l/cap) on each logit before the mask, the
+                                     model's epilogue (src/model.zig:2492-2514) fused into the read;
+                                     set it when the producer leaves logits uncapped.  V must be a
+                                     multiple of 32 (the reference's scalar tail is not restated). */
 } zi_params;
 
 /* Fills the reference defaults (src/sampler.zig:4-26). */

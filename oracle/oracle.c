@@ -33,6 +33,20 @@ void or_params_default(or_params *p) {
     p->xtc_probability = 0.0f;
     p->xtc_threshold = 0.1f;
     p->xtc_min_keep = 1;
+    p->final_logit_softcap = 0.0f;
+}
+
+/* The final-logit softcap of src/model.zig:2492-2510 (the vectorized body,
+ * i < 32*floor(V/32)): z = l * (1/cap) with 1/cap in f32, clamped to [-9, 9],
+ * e = exp(2z), tanh = (e - 1) / (e + 1), l = cap * tanh.  Every sequence step
+ * rounds to f32; exp is or_exp32. */
+float or_softcap(float l, float cap) {
+    const float inv_cap = 1.0f / cap;
+    /* @min(@max(z, -9), 9) lowers to maxnum/minnum: a NaN operand yields the other */
+    const float z = fminf(fmaxf(l * inv_cap, -9.0f), 9.0f);
+    const float e2z = or_exp32(z * 2.0f);
+    const float t = (e2z - 1.0f) / (e2z + 1.0f);
+    return cap * t;
 }
 
 /* src/sampler.zig:91-100.  Each distinct id of the window is penalized once
@@ -355,6 +369,14 @@ or_result or_sample_row(const or_params *p, float *logits, uint32_t V, const uin
                         const uint32_t *window, uint32_t n_window, const uint32_t *edit_ids,
                         const float *edit_deltas, uint32_t n_edits, const float *u,
                         or_sample_diag *diag) {
+    if (p->final_logit_softcap > 0.0f) { /* the model's epilogue, model.zig:2492-2514 */
+        const float cap = p->final_logit_softcap;
+        const uint32_t body = V / 32 * 32;
+        for (uint32_t i = 0; i < body; ++i) logits[i] = or_softcap(logits[i], cap);
+        /* the scalar tail calls std.math.tanh (:2511-2513), restated here with libm's tanhf:
+         * PARITY UNPINNED (no Zig); the product rejects V not a multiple of 32 */
+        for (uint32_t i = body; i < V; ++i) logits[i] = cap * tanhf(logits[i] / cap);
+    }
     if (mask) or_apply_mask(logits, V, mask); /* gen.zig:457-460: mask precedes sample */
     or_apply_penalty(logits, V, window, n_window, p->repeat_penalty, p->freq_penalty,
                      p->presence_penalty); /* sampler.zig:191 */

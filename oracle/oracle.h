@@ -69,6 +69,7 @@ typedef struct or_params {
     float    xtc_probability;
     float    xtc_threshold;
     uint32_t xtc_min_keep;
+    float    final_logit_softcap; /* 0 = off; applied to the row before the mask (src/model.zig:2492-2514) */
 } or_params;
 
 /* SampleResult, src/sampler.zig:527-530 */
@@ -180,6 +181,9 @@ typedef struct or_json {
     uint8_t object_only;
     uint8_t pad_;
 } or_json;
+
+/* model.zig:2492-2510 final-logit softcap, vectorized-body formula. */
+float  or_softcap(float l, float cap);
 
 void   or_json_init(or_json *j, int object_only);
 int    or_json_is_finished(const or_json *j);

@@ -34,6 +34,7 @@ class OrParams(C.Structure):
         ("xtc_probability", C.c_float),
         ("xtc_threshold", C.c_float),
         ("xtc_min_keep", C.c_uint32),
+        ("final_logit_softcap", C.c_float),
     ]
 
 
@@ -96,6 +97,8 @@ def lib():
             build()
         L = C.CDLL(_LIB_PATH)
         f32p, u32p = C.POINTER(C.c_float), C.POINTER(C.c_uint32)
+        L.or_softcap.restype = C.c_float
+        L.or_softcap.argtypes = [C.c_float, C.c_float]
         L.or_exp32.restype = C.c_float
         L.or_exp32.argtypes = [C.c_float]
         L.or_params_default.argtypes = [C.POINTER(OrParams)]
@@ -159,6 +162,10 @@ def params(**kw) -> OrParams:
             raise KeyError(k)
         setattr(p, k, v)
     return p
+
+
+def softcap(x: float, cap: float) -> float:
+    return lib().or_softcap(float(x), float(cap))
 
 
 def exp32(x: float) -> float:

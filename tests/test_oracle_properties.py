@@ -264,3 +264,58 @@ def test_apply_mask_bit_order(oracle):
     out = oracle.apply_mask(x, words)
     allowed = np.nonzero(np.isfinite(out))[0].tolist()
     assert allowed == [1, 3, 63, 64]
+
+
+# ------------------------------------------------------------------ final-logit softcap
+@pytest.mark.parametrize("cap", [30.0, 15.0, 50.0, 1.0])
+def test_softcap_is_tanh(oracle, cap):
+    """model.zig:2492-2510 computes cap*tanh(l/cap) through exp: within a few
+    f32 ulps of cap of the f64 closed form (a dropped factor 2, a wrong sign or
+    an unclamped exp fails by far more); |result| <= cap; odd within ulps."""
+    rng = np.random.default_rng(int(cap))
+    ls = np.concatenate([rng.standard_normal(2000) * cap * 2, rng.standard_normal(500) * 1e-3,
+                         np.linspace(-12 * cap, 12 * cap, 2001), [0.0, -0.0, 1e-30, -1e-30]]).astype(np.float32)
+    got = np.array([oracle.softcap(x, cap) for x in ls], np.float64)
+    want = cap * np.tanh(ls.astype(np.float64) / cap)
+    assert np.max(np.abs(got - want)) <= cap * 2.0 ** -22
+    assert np.all(np.abs(got) <= cap)
+    neg = np.array([oracle.softcap(-x, cap) for x in ls], np.float64)
+    assert np.max(np.abs(neg + got)) <= cap * 2.0 ** -22
+
+
+def test_softcap_saturates_and_special_values(oracle):
+    """|l| >= 9 cap clamps to the same value as l = +-9 cap; -inf gives the
+    low end (a masked, pruned logit stays finite until the mask); NaN takes
+    the -9 end, the maxnum rule of @max (a NaN operand yields the other)."""
+    cap = 30.0
+    hi, lo = oracle.softcap(9 * cap, cap), oracle.softcap(-9 * cap, cap)
+    assert hi == -lo and 0.9999 * cap < hi <= cap
+    for x in [9.5 * cap, 1e6, 3.4e38, np.inf]:
+        assert oracle.softcap(x, cap) == hi
+        assert oracle.softcap(-x, cap) == lo
+    assert oracle.softcap(float("nan"), cap) == lo
+    assert oracle.softcap(0.0, cap) == 0.0
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_softcap_precedes_mask_and_penalty(oracle, seed):
+    """The cap belongs to the forward (model.zig:2492), so it runs before the
+    grammar mask (gen.zig:457-460) and the penalties (sampler.zig:191):
+    sampling raw logits with the cap equals sampling the capped row without
+    it, and differs from capping after the penalty."""
+    rng = np.random.default_rng(seed)
+    V, cap = 320, 5.0
+    x = (rng.standard_normal(V) * 8).astype(np.float32)
+    win = np.argsort(-x)[:6].astype(np.uint32)
+    mask = rng.integers(0, 2**32, V // 32, dtype=np.uint64).astype(np.uint32)
+    mask[0] |= 1
+    pk = dict(temp=0.9, top_k=50, top_p=0.95, min_p=0.02, repeat_penalty=1.4, penalty_last_n=64)
+    capped = np.array([oracle.softcap(v, cap) for v in x], np.float32)
+    u = [0.37, 0.81]
+    t1, m1, d1 = oracle.sample_row(oracle.params(final_logit_softcap=cap, **pk), x, u, mask=mask, window=win, cap=50)
+    t2, m2, d2 = oracle.sample_row(oracle.params(**pk), capped, u, mask=mask, window=win, cap=50)
+    assert (t1, m1) == (t2, m2) and np.array_equal(d1["ids"], d2["ids"])
+    assert np.array_equal(d1["probs"], d2["probs"])
+    pen_first = oracle.apply_penalty(x, win, 1.4)
+    late = np.array([oracle.softcap(v, cap) for v in pen_first], np.float32)
+    assert not np.array_equal(late[win], oracle.apply_penalty(capped, win, 1.4)[win])

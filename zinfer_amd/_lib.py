@@ -44,6 +44,7 @@ class ZiParams(C.Structure):
         ("xtc_threshold", C.c_float),
         ("xtc_min_keep", C.c_uint32),
         ("seed", C.c_uint64),
+        ("final_logit_softcap", C.c_float),
     ]
 
 

@@ -48,6 +48,7 @@ extern "C" void zi_params_default(zi_params *p) {
     p->xtc_threshold = 0.1f;
     p->xtc_min_keep = 1;
     p->seed = 0;
+    p->final_logit_softcap = 0.0f;
 }
 
 #define HIP_TRY(call, what)                          \
@@ -192,6 +193,13 @@ static int32_t fill_source(const zi_batch *b, const zi_params *p, bool with_inpu
             return zi_fail(ZI_ERR_INVALID, "%s: mask_ld=%d < ceil(V/32)", fn, b->mask_ld);
         s.mask = b->mask;
         s.mask_ld = b->mask_ld;
+    }
+    if (p && p->final_logit_softcap > 0.0f) {
+        if (b->vocab % 32)
+            return zi_fail(ZI_ERR_UNSUPPORTED, "%s: final_logit_softcap with V=%d (not a multiple of 32)", fn,
+                           b->vocab);
+        s.cap = p->final_logit_softcap;
+        s.inv_cap = 1.0f / p->final_logit_softcap;
     }
     if (p) {
         s.rp = p->repeat_penalty;

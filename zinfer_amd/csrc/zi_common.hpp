@@ -42,6 +42,15 @@ __device__ __forceinline__ uint32_t ckey_id(uint64_t k) { return ~(uint32_t)(k &
 // result must agree bit-for-bit with the CPU oracle (oracle/or_exp32).
 __device__ __forceinline__ float exp32(float x) { return (float)exp((double)x); }
 
+// Final-logit softcap, the vectorized body of src/model.zig:2492-2510:
+// z = l * (1/cap) clamped to [-9, 9], tanh = (e - 1) / (e + 1) with e = exp(2z),
+// l = cap * tanh, every step rounded to f32.
+__device__ __forceinline__ float softcap_f(float l, float cap, float inv_cap) {
+    const float z = fminf(fmaxf(l * inv_cap, -9.0f), 9.0f);
+    const float e2z = exp32(z * 2.0f);
+    return cap * ((e2z - 1.0f) / (e2z + 1.0f));
+}
+
 __device__ __forceinline__ int lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0)); }
 
 // Number of set bits of `m` below this lane.

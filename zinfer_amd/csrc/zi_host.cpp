@@ -62,6 +62,18 @@ struct Xoshiro {
     }
 };
 
+// The final-logit softcap of src/model.zig:2492-2510 on a host row, in place
+// (the caller's logits then hold what the reference's forward leaves there).
+// Same f32 steps as the device's; V must be a multiple of 32.
+static void host_softcap(float *logits, uint32_t V, float cap) {
+    const float inv_cap = 1.0f / cap;
+    for (uint32_t i = 0; i < V; ++i) {
+        const float z = std::fmin(std::fmax(logits[i] * inv_cap, -9.0f), 9.0f);
+        const float e2z = (float)std::exp((double)(z * 2.0f));
+        logits[i] = cap * ((e2z - 1.0f) / (e2z + 1.0f));
+    }
+}
+
 // src/sampler.zig:91-100 plus the frequency/presence extension, on a host row.
 void host_penalty(float *logits, uint32_t V, const uint32_t *win, uint32_t n, const zi_params &p) {
     const bool rep = p.repeat_penalty != 1.0f;
@@ -285,9 +297,17 @@ extern "C" int32_t zi_sampler_sample_with_margin(zi_sampler *s, float *logits, u
     zi_ctx *c = s->ctx;
     char *h = (char *)s->st.h;
     char *d = (char *)s->st.d;
-    const zi_params &p = s->p;
+    zi_params p = s->p;
     if (p.penalty_last_n > (uint32_t)zi::kMaxWinHost)
         return zi_fail(ZI_ERR_UNSUPPORTED, "penalty_last_n %u > %d", p.penalty_last_n, zi::kMaxWinHost);
+    if (p.final_logit_softcap > 0.0f) {
+        // the caller's row is capped in place, as the reference's forward
+        // leaves it, so the device samples it with the cap off
+        if (n % 32)
+            return zi_fail(ZI_ERR_UNSUPPORTED, "final_logit_softcap with vocab %u (not a multiple of 32)", n);
+        host_softcap(logits, n, p.final_logit_softcap);
+        p.final_logit_softcap = 0.0f;
+    }
 
     std::memcpy(h + s->o_logits, logits, (size_t)n * 4);
     uint32_t *win = (uint32_t *)(h + s->o_hist);

@@ -38,6 +38,7 @@ struct RowSource {
     int edit_ld;
     float rp, freq, pres;
     int do_rep, do_fp;
+    float cap, inv_cap;  // final-logit softcap (cap > 0), applied first
 };
 
 struct SampleParams {

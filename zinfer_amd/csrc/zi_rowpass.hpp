@@ -203,7 +203,7 @@ __device__ __forceinline__ void pen_clear(PenTable &t, int c0, int c1) {
 // atomicOr set an id's bit owns that id and issues the reload of its logit
 // (row = logits row, mrow = mask row or null).  No barrier.
 template <typename T>
-__device__ __forceinline__ void pen_mark(PenTable &t, const PenRegs &pr, int c0, int c1, PenOwn &own, const T *row,
+__device__ __forceinline__ void pen_mark(const RowSource &a, PenTable &t, const PenRegs &pr, int c0, int c1, PenOwn &own, const T *row,
                                          const uint32_t *mrow) {
 #pragma unroll
     for (int u = 0; u < kOwnSlots; ++u) {
@@ -220,6 +220,7 @@ __device__ __forceinline__ void pen_mark(PenTable &t, const PenRegs &pr, int c0,
     for (int u = 0; u < kOwnSlots; ++u) {
         if (own.id[u] != 0xFFFFFFFFu) {
             float v = load_logit<T>(row, own.id[u]);
+            if (a.cap > 0.0f) v = softcap_f(v, a.cap, a.inv_cap);
             if (mrow && !((mrow[own.id[u] >> 5] >> (own.id[u] & 31)) & 1u)) v = -INFINITY;
             own.x[u] = v;
         }
@@ -323,7 +324,7 @@ __device__ __forceinline__ float chunk_stream(const RowSource &a, int row, int c
         rp = row_pen(a, row);
         pen_window(rp, pr);
         __syncthreads();  // tables cleared
-        pen_mark<T>(*t, pr, c0, c1, *own, reinterpret_cast<const T *>(a.logits) + (int64_t)row * a.ld, mrow);
+        pen_mark<T>(a, *t, pr, c0, c1, *own, reinterpret_cast<const T *>(a.logits) + (int64_t)row * a.ld, mrow);
         __syncthreads();  // bitset complete
 #pragma unroll
         for (int j = 0; j < NV; ++j) pw[j] = t->bits[(min(j * kThreads + tid, nvec - 1) * VEC) >> 5];
@@ -335,6 +336,10 @@ __device__ __forceinline__ float chunk_stream(const RowSource &a, int row, int c
         const int id0 = c0 + q * VEC;
         float v[VEC];
         unpack<T>(raw[j], v);
+        if (a.cap > 0.0f) {  // uniform
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) v[e] = softcap_f(v[e], a.cap, a.inv_cap);
+        }
         if (HAS_MASK) {
             uint32_t mb = mw[j] >> (id0 & 31);
 #pragma unroll
