@@ -38,6 +38,9 @@ def parse():
                          "verify: zi_sampler_verify")
     ap.add_argument("--softcap", type=float, default=0.0,
                     help="final-logit softcap fused into the read (sample path; 0 = off, the config's default)")
+    ap.add_argument("--pruned", type=int, default=0,
+                    help="pruned rows (sample path): 64 fixed + this many random groups of 8 ids per row are the "
+                         "only logits (zi_sample_rows_pruned; the reference keeps 512); 0 = dense rows")
     ap.add_argument("--rotate-mib", type=int, default=512, help="distinct input bytes cycled through")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample (0 = skip)")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
@@ -389,13 +392,27 @@ def main():
     mask = torch.from_numpy(w.mask).to(dev) if w.mask is not None else None
     uni = torch.from_numpy(w.uniforms).to(dev)
     p = params(**w.params)
+    gdev = cdev = None
+    if args.pruned > 0:  # the reference's candidate groups (src/model.zig:2070-2125): 0..63 + the rest
+        from oracle import pyoracle
+
+        grng = np.random.Generator(np.random.PCG64(909))
+        ngt = (V + 7) // 8
+        G = np.stack([np.concatenate([np.arange(64), grng.choice(np.arange(64, ngt), args.pruned, replace=False)])
+                      for _ in range(rows)]).astype(np.int32)
+        gdev = torch.from_numpy(G).to(dev)
+        cdev = torch.full((rows,), G.shape[1], dtype=torch.int32, device=dev)
+        # the CPU leg samples the rows as the reference sees them: -inf outside the groups
+        w.logits = np.stack([pyoracle.pruned_row(w.logits[r], G[r], V) for r in range(rows)])
+        w.name += f"_pruned{G.shape[1]}"
     ctx = Context(0, max_rows=max(rows, 64), max_vocab=V)
     outs = [SampleResult(tok=torch.empty(rows, dtype=torch.int32, device=dev),
                          margin=torch.empty(rows, dtype=torch.float32, device=dev),
                          ndraws=torch.empty(rows, dtype=torch.int32, device=dev)) for _ in range(nsets)]
 
     def launch(i):
-        ctx.sample_rows(p, sets[i], uni, vocab=V, hist=hist, hist_len=hist_len, mask=mask, out=outs[i])
+        ctx.sample_rows(p, sets[i], uni, vocab=V, hist=hist, hist_len=hist_len, mask=mask, out=outs[i],
+                        groups=gdev, group_count=cdev)
 
     stream = torch.cuda.Stream(dev)  # default priority
     with torch.cuda.stream(stream):
@@ -436,12 +453,19 @@ def main():
     ms_per_step = gpu_ms / steps
     rows_per_s = rows / (ms_per_step * 1e-3)
     nbytes = w.nbytes()
+    if gdev is not None:  # per row: the listed groups' logits, their ids, the count, history, mask bits,
+        ng = gdev.shape[1]  # one uniform, token + margin
+        per_row = ng * (8 * elt + 4) + 4 + ((w.hist.shape[1] * 4 + 4) if w.hist is not None else 0) \
+            + (ng if w.mask is not None else 0) + 4 + 8
+        nbytes = rows * per_row
     achieved = nbytes / (ms_per_step * 1e-3) / 1e9
     top_k = w.params.get("top_k", 40)
     k_eff = V if (top_k == 0 or top_k > V) else top_k
     # the launch's dominant kernel: batches of >= 256 rows (kRowLoopRows in zi_sample.hip) run one
     # workgroup per row
-    if rows >= 256:
+    if gdev is not None:
+        kernel = "pruned_kernel"
+    elif rows >= 256:
         kernel = "row_kernel"
     else:
         kernel = "nucleus_kernel" if k_eff > 256 else "sample_kernel"
@@ -451,7 +475,8 @@ def main():
     ref = SampleResult(tok=torch.empty(rows, dtype=torch.int32, device=dev),
                        margin=torch.empty(rows, dtype=torch.float32, device=dev),
                        ndraws=torch.empty(rows, dtype=torch.int32, device=dev))
-    ctx.sample_rows(p, sets[0], uni, vocab=V, hist=hist, hist_len=hist_len, mask=mask, out=ref)
+    ctx.sample_rows(p, sets[0], uni, vocab=V, hist=hist, hist_len=hist_len, mask=mask, out=ref, groups=gdev,
+                    group_count=cdev)
     torch.cuda.synchronize()
     assert torch.equal(ref.tok, outs[0].tok) and torch.equal(ref.margin, outs[0].margin), "replay differs from eager"
 

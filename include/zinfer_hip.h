@@ -150,6 +150,23 @@ typedef struct zi_sample_out {
 int32_t zi_sample_rows(zi_ctx *ctx, const zi_params *p, const zi_batch *b,
                        const float *uniforms, const zi_sample_out *out);
 
+/* zi_sample_rows on pruned-vocabulary rows.  Replaces the reference's -inf
+ * fill of the whole logit row (src/model.zig:2127-2128) plus the full read of
+ * it: the pruned lm_head (:2036-2140) computes only its candidate groups of 8
+ * ids (prunedFineWorker, :1144-1160, writing logits[8g .. 8g + 8)), and this
+ * entry reads only those, every other id being -inf.  groups [rows][groups_ld]
+ * lists row r's group ids g (ids [8g, 8g + 8) valid in `b`'s row, the rest of
+ * the row is never read); group_count [rows] (device) how many, clamped to
+ * groups_ld.  Ids g >= ceil(V / 8) are ignored; a group listed twice counts
+ * once.  Results are those of zi_sample_rows on the row with the fill
+ * written.  Limits: groups_ld <= 1024 (the reference keeps 576), V >= 16,
+ * top_k resolving to <= 256 when temp > 0, no final_logit_softcap (it would
+ * move the fill to -cap); each returns ZI_ERR_UNSUPPORTED. */
+int32_t zi_sample_rows_pruned(zi_ctx *ctx, const zi_params *p, const zi_batch *b,
+                              const uint32_t *groups, const int32_t *group_count,
+                              int32_t groups_ld, const float *uniforms,
+                              const zi_sample_out *out);
+
 /* argmaxWithMargin per row (src/sampler.zig:532-614; greedy decoding, the
  * bench argmax at src/main.zig:690).  out_tok/out_margin follow the reference
  * 2x8-lane rules; out_tok_low/out_margin_true (may be NULL) give the

@@ -360,3 +360,18 @@ def bench_json_mask(states, piece_off, piece_buf, eog, eos, reps: int):
                                  _p(e, C.c_uint32), e.size, -1 if eos is None else int(eos),
                                  _p(out, C.c_uint32), reps)
     return t, out
+
+
+def pruned_row(logits, groups, V: int) -> np.ndarray:
+    """The row the reference's pruned lm_head leaves: the whole row is set to
+    -inf (src/model.zig:2127-2128), then prunedFineWorker (:1144-1160) writes
+    logits[8g .. 8g + 8) for each candidate group g.  Groups past the
+    vocabulary are skipped; a repeated group writes the same values again."""
+    row = np.full(V, -np.inf, np.float32)
+    g = np.asarray(groups, np.int64)
+    g = g[(g >= 0) & (g < (V + 7) // 8)]
+    if g.size:
+        ids = (g[:, None] * 8 + np.arange(8)[None, :]).reshape(-1)
+        ids = ids[ids < V]
+        row[ids] = np.asarray(logits, np.float32)[ids]
+    return row

@@ -121,6 +121,8 @@ SIGNATURES = {
     "zi_abi_version": (C.c_int32, []),
     "zi_sample_rows": (C.c_int32, [C.c_void_p, C.POINTER(ZiParams), C.POINTER(ZiBatch), C.c_void_p,
                                     C.POINTER(ZiSampleOut)]),
+    "zi_sample_rows_pruned": (C.c_int32, [C.c_void_p, C.POINTER(ZiParams), C.POINTER(ZiBatch), C.c_void_p,
+                                           C.c_void_p, C.c_int32, C.c_void_p, C.POINTER(ZiSampleOut)]),
     "zi_argmax_rows": (C.c_int32, [C.c_void_p, C.POINTER(ZiBatch), C.c_void_p, C.c_void_p, C.c_void_p,
                                     C.c_void_p]),
     "zi_entropy_topk_rows": (C.c_int32, [C.c_void_p, C.POINTER(ZiBatch), C.c_int32, C.c_void_p, C.c_void_p,

@@ -88,7 +88,10 @@ class Context:
 
     def sample_rows(self, p: ZiParams, logits: torch.Tensor, uniforms: torch.Tensor, *, vocab=None, hist=None,
                     hist_len=None, mask=None, edit_ids=None, edit_delta=None, edit_count=None,
-                    cands: bool = False, out: Optional[SampleResult] = None) -> SampleResult:
+                    cands: bool = False, out: Optional[SampleResult] = None, groups=None,
+                    group_count=None) -> SampleResult:
+        """zi_sample_rows; with `groups` ([rows, ld] int32/uint32 group ids) and
+        `group_count` ([rows] int32), zi_sample_rows_pruned."""
         rows = logits.shape[0]
         dev = logits.device
         if out is None:
@@ -111,7 +114,11 @@ class Context:
             o.cand_ld = out.cand_ids.stride(0)
         b = self.batch(logits, vocab, hist, hist_len, mask, edit_ids, edit_delta, edit_count)
         self._bind_stream()
-        check(lib().zi_sample_rows(self.h, C.byref(p), C.byref(b), _ptr(uniforms), C.byref(o)))
+        if groups is not None:
+            check(lib().zi_sample_rows_pruned(self.h, C.byref(p), C.byref(b), _ptr(groups), _ptr(group_count),
+                                              groups.stride(0), _ptr(uniforms), C.byref(o)))
+        else:
+            check(lib().zi_sample_rows(self.h, C.byref(p), C.byref(b), _ptr(uniforms), C.byref(o)))
         return out
 
     def argmax_rows(self, logits: torch.Tensor, vocab=None):

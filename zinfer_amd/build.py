@@ -17,7 +17,8 @@ CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libzinfer_hip.so")
 OBJ = os.path.join(ROOT, "_build", "obj")
 
-SOURCES = ["zi_sample.hip", "zi_exact.hip", "zi_argmax.hip", "zi_entropy.hip", "zi_grammar.hip", "zi_api.cpp",
+SOURCES = ["zi_sample.hip", "zi_sample_cap.hip", "zi_exact.hip", "zi_argmax.hip", "zi_entropy.hip", "zi_grammar.hip", "zi_pruned.hip",
+           "zi_api.cpp",
            "zi_host.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

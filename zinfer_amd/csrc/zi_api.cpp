@@ -395,6 +395,69 @@ extern "C" int32_t zi_sample_rows(zi_ctx *c, const zi_params *p, const zi_batch 
     return ZI_OK;
 }
 
+extern "C" int32_t zi_sample_rows_pruned(zi_ctx *c, const zi_params *p, const zi_batch *b, const uint32_t *groups,
+                                         const int32_t *group_count, int32_t groups_ld, const float *uniforms,
+                                         const zi_sample_out *out) {
+    const char *fn = "zi_sample_rows_pruned";
+    int32_t rc = check_batch(c, b, fn);
+    if (rc) return rc;
+    if (!p || !out || !out->tok || !out->margin) return zi_fail(ZI_ERR_INVALID, "%s: NULL params/out/tok/margin", fn);
+    if (!groups || !group_count || groups_ld < 1)
+        return zi_fail(ZI_ERR_INVALID, "%s: groups/group_count NULL or groups_ld=%d", fn, groups_ld);
+    if (groups_ld > zi::kMaxGroupsHost)
+        return zi_fail(ZI_ERR_UNSUPPORTED, "%s: groups_ld=%d > %d", fn, groups_ld, zi::kMaxGroupsHost);
+    if (b->vocab < 16) return zi_fail(ZI_ERR_UNSUPPORTED, "%s: vocab %d < 16", fn, b->vocab);
+    if (p->final_logit_softcap > 0.0f)  // the cap (model.zig:2492) runs after the fill (:2127) and moves it to -cap
+        return zi_fail(ZI_ERR_UNSUPPORTED, "%s: final_logit_softcap with pruned rows", fn);
+    HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+    const zi::Plan pl = zi::plan_rows(b->rows, b->vocab, b->dtype);
+    zi::RowSource src;
+    rc = fill_source(b, p, true, src, pl, fn);
+    if (rc) return rc;
+    if (src.hist && src.hist_ld > zi::kMaxWinHost) {  // the kernel prefetches whole history rows
+        hipError_t e = zi::launch_window_compact(src.hist, src.hist_len, src.hist_ld, src.win, b->rows, c->win_ids,
+                                                 c->win_len, c->stream);
+        if (e != hipSuccess) return zi_hip_fail(e, "window compaction launch");
+        src.hist = c->win_ids;
+        src.hist_len = c->win_len;
+        src.hist_ld = zi::kMaxWinHost;
+    }
+    const uint32_t V = (uint32_t)b->vocab;
+    const uint32_t k = (p->top_k == 0 || p->top_k > V) ? V : p->top_k;  // src/sampler.zig:197
+    if (p->temp > 0.0f) {
+        if (!uniforms) return zi_fail(ZI_ERR_INVALID, "%s: uniforms is NULL", fn);
+        if (k > (uint32_t)zi::kMaxTopK)
+            return zi_fail(ZI_ERR_UNSUPPORTED, "%s: top_k resolves to %u > %d", fn, k, zi::kMaxTopK);
+        if ((out->cand_ids || out->cand_vals || out->probs) && out->cand_ld < (int32_t)k)
+            return zi_fail(ZI_ERR_INVALID, "%s: cand_ld=%d < k=%u", fn, out->cand_ld, k);
+    }
+    zi::SampleParams P;
+    std::memset(&P, 0, sizeof P);
+    P.src = src;
+    P.k = (int)(k > (uint32_t)zi::kMaxTopK ? (uint32_t)zi::kMaxTopK : k);
+    P.temp = p->temp;
+    P.top_p = p->top_p;
+    P.min_p = p->min_p;
+    P.xtc_p = p->xtc_probability;
+    P.xtc_thr = p->xtc_threshold;
+    P.xtc_min_keep = (int)(p->xtc_min_keep > 0x7FFFFFFFu ? 0x7FFFFFFFu : p->xtc_min_keep);
+    P.uniforms = p->temp > 0.0f ? uniforms : nullptr;
+    P.tok = out->tok;
+    P.margin = out->margin;
+    P.ndraws = out->ndraws;
+    P.keep = out->keep;
+    P.cand_ids = out->cand_ids;
+    P.cand_vals = out->cand_vals;
+    P.probs = out->probs;
+    P.cand_ld = out->cand_ld;
+    P.groups = groups;
+    P.group_count = group_count;
+    P.groups_ld = groups_ld;
+    hipError_t e = zi::launch_pruned(P, b->dtype, b->rows, c->stream);
+    if (e != hipSuccess) return zi_hip_fail(e, "pruned kernel launch");
+    return ZI_OK;
+}
+
 extern "C" int32_t zi_argmax_rows(zi_ctx *c, const zi_batch *b, uint32_t *out_tok, float *out_margin,
                                   uint32_t *out_tok_low, float *out_margin_true) {
     int32_t rc = check_batch(c, b, "zi_argmax_rows");

@@ -37,7 +37,7 @@ struct ArgPenLds {
 template <>
 struct ArgPenLds<false> {};
 
-template <typename T, int NV, bool HAS_MASK, bool HAS_PEN>
+template <typename T, int NV, bool HAS_MASK, bool HAS_PEN, bool CAP>
 __global__ __launch_bounds__(kThreads) void argmax_kernel(ArgmaxParams P) {
     __shared__ ArgPenLds<HAS_PEN> pl;
     __shared__ unsigned long long s_ck[16];
@@ -65,7 +65,7 @@ __global__ __launch_bounds__(kThreads) void argmax_kernel(ArgmaxParams P) {
         s_tail[tid] = __builtin_nanf("");
     }
     ChunkRegs<T, NV> cr;
-    chunk_stream<T, NV, HAS_MASK, HAS_PEN>(a, row, c0, c1, cr, pen, &own);
+    chunk_stream<T, NV, HAS_MASK, HAS_PEN, CAP>(a, row, c0, c1, cr, pen, &own);
     __syncthreads();  // s_* initialised
 
     // per-thread class records (thread t only meets classes (t*VEC + e) & 15)
@@ -249,7 +249,8 @@ __global__ __launch_bounds__(kThreads) void argmax_kernel(ArgmaxParams P) {
 template <typename T, int NV, bool M, bool PN>
 static hipError_t launch_argmax_t(const ArgmaxParams &P, int rows, hipStream_t st) {
     dim3 grid(rows * P.src.G), block(kThreads);
-    hipLaunchKernelGGL((argmax_kernel<T, NV, M, PN>), grid, block, 0, st, P);
+    if (P.src.cap > 0.0f) hipLaunchKernelGGL((argmax_kernel<T, NV, M, PN, true>), grid, block, 0, st, P);
+    else hipLaunchKernelGGL((argmax_kernel<T, NV, M, PN, false>), grid, block, 0, st, P);
     return hipGetLastError();
 }
 

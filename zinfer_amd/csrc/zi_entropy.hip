@@ -75,8 +75,8 @@ __global__ __launch_bounds__(kThreads) void entropy_kernel(EntropyParams P) {
 
     ChunkRegs<T, NV> cr;
     float ref = -INFINITY, S = 0.0f, U = 0.0f;
-    chunk_stream<T, NV, false, false, EntHook>(a, row, c0, c1, cr, nullptr, nullptr,
-                                               EntHook{&ref, &S, &U});
+    chunk_stream<T, NV, false, false, false, EntHook>(a, row, c0, c1, cr, nullptr, nullptr,
+                                                      EntHook{&ref, &S, &U});
 
     // workgroup merge of (ref, S, U) in f64
     float wm = wave_max_f(ref);

@@ -82,14 +82,14 @@ __device__ __forceinline__ float exact_penalize(const ExactPenLds &t, const RowS
 
 // The VEC logits of vector q of the row after mask and penalties; ids >= V
 // become NaN.
-template <typename T, bool HAS_MASK, bool HAS_PEN>
+template <typename T, bool HAS_MASK, bool HAS_PEN, bool CAP>
 __device__ __forceinline__ void exact_vector(const RowSource &a, int row, const ExactPenLds &t, int hs_log2, int q,
                                              float (&v)[VecTraits<T>::VEC]) {
     constexpr int VEC = VecTraits<T>::VEC;
     const T *base = reinterpret_cast<const T *>(a.logits) + (int64_t)row * a.ld;
     const int id0 = q * VEC;
     unpack<T>(*reinterpret_cast<const uint4 *>(base + id0), v);
-    if (a.cap > 0.0f) {
+    if constexpr (CAP) {
 #pragma unroll
         for (int e = 0; e < VEC; ++e) v[e] = softcap_f(v[e], a.cap, a.inv_cap);
     }
@@ -386,7 +386,7 @@ __device__ __forceinline__ uint32_t key_floor(float mx, float dlo) {
     return ~okey(f);
 }
 
-template <typename T, bool HAS_MASK, bool HAS_PEN>
+template <typename T, bool HAS_MASK, bool HAS_PEN, bool CAP>
 __global__ __launch_bounds__(kThreads) void exact_kernel(ExactParams P) {
     __shared__ ExactLds sm;
     __shared__ uint32_t s_hist[4][256];  // counts of each digit over the entries being sorted
@@ -442,7 +442,7 @@ __global__ __launch_bounds__(kThreads) void exact_kernel(ExactParams P) {
     float t1 = -INFINITY, t2 = -INFINITY;
     for (int q = tid; q < nvec; q += kThreads) {
         float v[VEC];
-        exact_vector<T, HAS_MASK, HAS_PEN>(a, row, sm.pen, rp.hs_log2, q, v);
+        exact_vector<T, HAS_MASK, HAS_PEN, CAP>(a, row, sm.pen, rp.hs_log2, q, v);
         uint32_t kk[VEC];
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
@@ -681,7 +681,8 @@ __global__ __launch_bounds__(kThreads) void exact_kernel(ExactParams P) {
 
 template <typename T, bool M, bool PN>
 static hipError_t launch_exact_t(const ExactParams &P, int rows, hipStream_t st) {
-    hipLaunchKernelGGL((exact_kernel<T, M, PN>), dim3(rows), dim3(kThreads), 0, st, P);
+    if (P.src.cap > 0.0f) hipLaunchKernelGGL((exact_kernel<T, M, PN, true>), dim3(rows), dim3(kThreads), 0, st, P);
+    else hipLaunchKernelGGL((exact_kernel<T, M, PN, false>), dim3(rows), dim3(kThreads), 0, st, P);
     return hipGetLastError();
 }
 

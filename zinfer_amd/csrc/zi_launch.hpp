@@ -15,6 +15,7 @@ constexpr int kMaxWinHost = 1024;   // penalty window
 constexpr int kMaxEditsHost = 128;  // sparse edits per row
 constexpr int kMaxTopK = 256;
 constexpr int kMaxEntropyK = 64;
+constexpr int kMaxGroupsHost = 1024;  // listed groups of 8 per pruned row (the reference keeps <= 576)
 
 struct Plan {
     int G, CH, nv;
@@ -63,6 +64,10 @@ struct SampleParams {
     int n_all;          // the reference's candidate count (V)
     double *g_stat;     // [rows][G][3]: chunk max, sum exp(x - max)
     int32_t *nuc_flag;  // [rows] out: 1 = keep not fixed by the prefix, run exact_kernel
+    // pruned rows (pruned_kernel only): ids [8g, 8g + 8) of the listed groups g
+    const uint32_t *groups;      // [rows][groups_ld]
+    const int32_t *group_count;  // [rows]
+    int groups_ld;
 };
 
 // Exact whole-order sampling of one row per workgroup (top_k = 0 rows the
@@ -129,6 +134,10 @@ struct MaskParams {
 
 hipError_t launch_sample(const SampleParams &P, int dtype, int nv, int rows, hipStream_t st);
 hipError_t launch_nucleus(const SampleParams &P, int dtype, int nv, int rows, hipStream_t st);
+hipError_t launch_pruned(const SampleParams &P, int dtype, int rows, hipStream_t st);
+// the final-logit softcap instances of launch_sample / launch_nucleus (zi_sample_cap.hip)
+hipError_t launch_sample_capped(const SampleParams &P, int dtype, int nv, int rows, hipStream_t st);
+hipError_t launch_nucleus_capped(const SampleParams &P, int dtype, int nv, int rows, hipStream_t st);
 hipError_t launch_exact(const ExactParams &P, int dtype, int rows, hipStream_t st);
 hipError_t launch_argmax(const ArgmaxParams &P, int dtype, int nv, int rows, hipStream_t st);
 hipError_t launch_entropy(const EntropyParams &P, int dtype, int nv, int rows, hipStream_t st);

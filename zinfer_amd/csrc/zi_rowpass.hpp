@@ -201,8 +201,9 @@ __device__ __forceinline__ void pen_clear(PenTable &t, int c0, int c1) {
 
 // Marks the chunk's penalized/edited ids in the bitset; the thread whose
 // atomicOr set an id's bit owns that id and issues the reload of its logit
-// (row = logits row, mrow = mask row or null).  No barrier.
-template <typename T>
+// (row = logits row, mrow = mask row or null).  CAP: the reloaded logit gets
+// the final-logit softcap.  No barrier.
+template <typename T, bool CAP>
 __device__ __forceinline__ void pen_mark(const RowSource &a, PenTable &t, const PenRegs &pr, int c0, int c1, PenOwn &own, const T *row,
                                          const uint32_t *mrow) {
 #pragma unroll
@@ -220,7 +221,7 @@ __device__ __forceinline__ void pen_mark(const RowSource &a, PenTable &t, const 
     for (int u = 0; u < kOwnSlots; ++u) {
         if (own.id[u] != 0xFFFFFFFFu) {
             float v = load_logit<T>(row, own.id[u]);
-            if (a.cap > 0.0f) v = softcap_f(v, a.cap, a.inv_cap);
+            if constexpr (CAP) v = softcap_f(v, a.cap, a.inv_cap);
             if (mrow && !((mrow[own.id[u] >> 5] >> (own.id[u] & 31)) & 1u)) v = -INFINITY;
             own.x[u] = v;
         }
@@ -293,11 +294,14 @@ struct NoMid {
     __device__ void operator()(float) const {}
 };
 
+// CAP: every value gets the final-logit softcap (a.cap > 0) right after it is
+// unpacked; instances without it carry no softcap code.
 // SPLIT < NV: after vector SPLIT-1 is processed, mid(partial lane max) runs
 // (the penalty hash is filled just before it) while the remaining vectors'
 // loads are still in flight; workgroup barriers inside mid order LDS only and
 // do not wait for them.
-template <typename T, int NV, bool HAS_MASK, bool HAS_PEN, class Hook = NoHook, int SPLIT = NV, class Mid = NoMid>
+template <typename T, int NV, bool HAS_MASK, bool HAS_PEN, bool CAP = false, class Hook = NoHook, int SPLIT = NV,
+          class Mid = NoMid>
 __device__ __forceinline__ float chunk_stream(const RowSource &a, int row, int c0, int c1, ChunkRegs<T, NV> &cr,
                                               PenTable *t, PenOwn *own, Hook hook = Hook(), Mid mid = Mid()) {
     constexpr int VEC = VecTraits<T>::VEC;
@@ -324,7 +328,7 @@ __device__ __forceinline__ float chunk_stream(const RowSource &a, int row, int c
         rp = row_pen(a, row);
         pen_window(rp, pr);
         __syncthreads();  // tables cleared
-        pen_mark<T>(a, *t, pr, c0, c1, *own, reinterpret_cast<const T *>(a.logits) + (int64_t)row * a.ld, mrow);
+        pen_mark<T, CAP>(a, *t, pr, c0, c1, *own, reinterpret_cast<const T *>(a.logits) + (int64_t)row * a.ld, mrow);
         __syncthreads();  // bitset complete
 #pragma unroll
         for (int j = 0; j < NV; ++j) pw[j] = t->bits[(min(j * kThreads + tid, nvec - 1) * VEC) >> 5];
@@ -336,7 +340,7 @@ __device__ __forceinline__ float chunk_stream(const RowSource &a, int row, int c
         const int id0 = c0 + q * VEC;
         float v[VEC];
         unpack<T>(raw[j], v);
-        if (a.cap > 0.0f) {  // uniform
+        if constexpr (CAP) {
 #pragma unroll
             for (int e = 0; e < VEC; ++e) v[e] = softcap_f(v[e], a.cap, a.inv_cap);
         }
