@@ -33,7 +33,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=2048)
     ap.add_argument("--warmup", type=int, default=128)
     ap.add_argument("--config", type=int, default=2, help="BASELINE config to run (2 = headline)")
-    ap.add_argument("--path", choices=["sample", "json_mask", "verify"], default="sample",
+    ap.add_argument("--path", choices=["sample", "json_mask", "verify", "dry"], default="sample",
                     help="sample: zi_sample_rows on --config (the headline); json_mask: zi_json_mask_rows; "
                          "verify: zi_sampler_verify")
     ap.add_argument("--softcap", type=float, default=0.0,
@@ -264,6 +264,100 @@ def bench_verify(args):
     ctx.close()
 
 
+def bench_dry(args):
+    """DRY edits on the device (zi_dry_edits_rows, src/sampler.zig:104-187) for 64
+    rows of 1024-token histories (the default dry_range), graph-replayed with
+    HIP events on the launch stream.  The histories mix Zipf ids with repeated
+    phrases, so every row has repeats to penalize.  Also timed: the worst case,
+    period-1 loops over the full 4096-token ring (dry_range 4096)."""
+    import numpy as np
+    import torch
+
+    from zinfer_amd.api import Context, params
+
+    rows, H = 64, 1024
+    rng = np.random.Generator(np.random.PCG64(616))
+    hist = np.minimum(rng.zipf(1.2, (rows, H)), 50000).astype(np.uint32)
+    for r in range(rows):  # paste a few earlier phrases again
+        for _ in range(8):
+            ln = int(rng.integers(3, 24))
+            a0 = int(rng.integers(0, H - 2 * ln))
+            b0 = int(rng.integers(a0 + ln, H - ln))
+            hist[r, b0:b0 + ln] = hist[r, a0:a0 + ln]
+    hl = np.full(rows, H, np.int32)
+    brk = np.array([13, 10, 2, 7], np.uint32)
+    pk = dict(dry_multiplier=0.8, dry_base=1.75, dry_allowed_length=2, dry_range=1024)
+    p = params(**pk)
+    dev = torch.device("cuda:0")
+    ctx = Context(0, max_rows=rows, max_vocab=1024)
+    hd, ld, bd = torch.from_numpy(hist).to(dev), torch.from_numpy(hl).to(dev), torch.from_numpy(brk).to(dev)
+
+    def timed(hd, ld, p, steps):
+        stream = torch.cuda.Stream(dev)
+        with torch.cuda.stream(stream):
+            out = ctx.dry_edits_rows(p, hd, ld, bd)
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                for _ in range(16):
+                    ctx.dry_edits_rows(p, hd, ld, bd)
+            torch.cuda.synchronize()
+            reps = max(1, steps // 16)
+            for _ in range(max(1, args.warmup // 16)):
+                graph.replay()
+            torch.cuda.synchronize()
+            ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            ev0.record(stream)
+            for _ in range(reps):
+                graph.replay()
+            ev1.record(stream)
+            torch.cuda.synchronize()
+        return ev0.elapsed_time(ev1) / (reps * 16), reps * 16, out
+
+    t0 = time.perf_counter()
+    ms, steps, (ids, dl, cnt) = timed(hd, ld, p, args.steps)
+    wall = time.perf_counter() - t0
+    worst = np.tile(np.uint32(5), (rows, 4096))
+    ms_worst, _, _ = timed(torch.from_numpy(worst).to(dev), torch.full((rows,), 4096, dtype=torch.int32, device=dev),
+                           params(**dict(pk, dry_range=4096)), 64)
+    from oracle import pyoracle
+
+    cnt_h = cnt.cpu().numpy()
+    ids_h = ids.cpu().numpy().astype(np.uint32)
+    parity = all(np.array_equal(ids_h[r, :cnt_h[r]], pyoracle.dry_edits(hist[r], brk, 0.8, 1.75, 2, 1024)[0])
+                 for r in range(rows))
+    cpu = None
+    if args.cpu_seconds > 0:
+        n_cpu, tc0 = 0, time.perf_counter()
+        while time.perf_counter() - tc0 < min(args.cpu_seconds, 10.0):
+            pyoracle.dry_edits(hist[n_cpu % rows], brk, 0.8, 1.75, 2, 1024)
+            n_cpu += 1
+        tc = time.perf_counter() - tc0
+        cpu = {"value": round(n_cpu / tc, 1), "unit": "rows/s", "cores": 1, "kind": "port",
+               "sample": f"{n_cpu} rows of the same histories ({tc:.1f} s), oracle/oracle.c or_dry_edits "
+                         f"(C restatement of src/sampler.zig:104-187, Z-algorithm), 1 thread"}
+    nbytes = rows * (H * 4 + 4) + int(cnt_h.sum()) * 8 + rows * 4
+    achieved = nbytes / (ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "DRY edit rows/sec (zi_dry_edits_rows, 64 rows x 1024-token histories)",
+        "value": round(rows / (ms * 1e-3), 1), "unit": "rows/s", "n_gpus": 1, "steps": steps,
+        "warmup": max(1, args.warmup // 16) * 16, "ms_per_step": round(ms, 6), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "u32",
+        "data": "synthetic, seeded (bench.py bench_dry): Zipf(1.2) ids with pasted phrases",
+        "config": {"workload": "dry_64x1024", "rows": rows, "history": H, **pk, "breakers": len(brk),
+                   "edits_mean": float(cnt_h.mean()), "worst_case_ms": round(ms_worst, 4),
+                   "worst_case": "period-1 loop, 4096-token ring, dry_range 4096", "parity_vs_oracle": parity},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": nbytes, "kernel": "dry_kernel"},
+        "cpu_baseline": cpu,
+        "wall_s": round(wall, 3),
+    }), flush=True)
+    ctx.close()
+    if not parity:
+        raise SystemExit("dry: device edits differ from the oracle")
+
+
 def bench_entropy(args, w):
     """Config 4: entropy (nats, T = 1, full vocabulary), top-8 ids and full-vocabulary
     probabilities, argmax and accept = (argmax == draft) per row
@@ -360,6 +454,9 @@ def main():
         return
     if args.path == "verify":
         bench_verify(args)
+        return
+    if args.path == "dry":
+        bench_dry(args)
         return
 
     import numpy as np

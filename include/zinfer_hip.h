@@ -292,6 +292,21 @@ float   zi_sampler_rand_f32(zi_sampler *s);
 int32_t zi_argmax_with_margin(zi_ctx *ctx, const float *logits, uint32_t n, uint32_t *tok,
                               float *margin);
 
+/* Sampler.applyDry (src/sampler.zig:104-187) for a batch on the device: the
+ * DRY edits of each row's history, written in the zi_batch.edit_* format so
+ * that zi_sample_rows applies them (logits[id] -= delta).  hist [rows][hist_ld]
+ * holds each row's accepted ids oldest first, hist_len [rows] how many (the
+ * last min(hist_len, dry_range, 4096) are searched, the reference's ring);
+ * breakers (device, <= 16, sampler.zig:32) the sequence breakers.  Writes
+ * out_count[r] (<= 128) and, when DRY is on, out_ids / out_delta
+ * [rows][edit_ld], edit_ld >= 128, in the reference's order (first
+ * appearance).  The same results as zi_dry_edits per row.  Asynchronous on
+ * the context's stream. */
+int32_t zi_dry_edits_rows(zi_ctx *ctx, const zi_params *p, const uint32_t *hist,
+                          const int32_t *hist_len, int32_t hist_ld, int32_t rows,
+                          const uint32_t *breakers, uint32_t n_breakers, uint32_t *out_ids,
+                          float *out_delta, int32_t *out_count, int32_t edit_ld);
+
 /* DRY edits (src/sampler.zig:104-187) from a linear history (oldest first),
  * as (id, delta) pairs for zi_batch.edit_*; returns the count (<= 128). */
 uint32_t zi_dry_edits(const uint32_t *hist, uint32_t n_hist, const uint32_t *breakers,

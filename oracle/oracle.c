@@ -14,6 +14,65 @@
 #include <time.h>
 
 float or_exp32(float x) { return (float)exp((double)x); }
+float or_log32(float x) { return (float)log((double)x); }
+
+/* std.math.pow(f32, x, y) as Zig computes it (src/sampler.zig:182 calls it for
+ * the DRY penalty).  Zig's lib/std/math/pow.zig (Zig 0.17.1, not in the
+ * reference tree) restates Go's math.Pow: special cases; x^yf = exp(yf*log(x))
+ * for the fractional part (yf moved into (-0.5, 0.5]); x^yi by repeated
+ * squaring of frexp(x)'s significand in f32 with the binary exponent carried
+ * separately (overflow guard at |xe| > 2^9 for f32); 1/a for y < 0; scalbn.
+ * exp/log: or_exp32 / or_log32.  Last-ulp agreement with Zig is PARITY
+ * UNPINNED (no Zig toolchain); the special cases, integer powers and the
+ * fractional split are pinned in tests. */
+static int pow_odd_int(float y) {
+    if (!(fabsf(y) < 16777216.0f)) return 0;
+    float t = truncf(y);
+    return t == y && fmodf(t, 2.0f) != 0.0f;
+}
+
+float or_pow_zig(float x, float y) {
+    if (y == 0.0f || x == 1.0f) return 1.0f;
+    if (isnan(x) || isnan(y)) return NAN;
+    if (y == 1.0f) return x;
+    if (x == 0.0f) {
+        if (y < 0.0f) return pow_odd_int(y) ? copysignf(INFINITY, x) : INFINITY;
+        return pow_odd_int(y) ? x : 0.0f;
+    }
+    if (isinf(y)) {
+        if (x == -1.0f) return 1.0f;
+        return ((fabsf(x) < 1.0f) == (y > 0.0f)) ? 0.0f : INFINITY;
+    }
+    if (isinf(x)) {
+        if (x < 0.0f) return or_pow_zig(1.0f / x, -y);
+        return y < 0.0f ? 0.0f : INFINITY;
+    }
+    if (y == 0.5f) return sqrtf(x);
+    if (y == -0.5f) return 1.0f / sqrtf(x);
+    float yi, yf = modff(fabsf(y), &yi);
+    if (yf != 0.0f && x < 0.0f) return NAN;
+    if (yi >= 2147483648.0f) {
+        if (x == -1.0f) return 1.0f;
+        return ((fabsf(x) < 1.0f) == (y > 0.0f)) ? 0.0f : INFINITY;
+    }
+    float a1 = 1.0f;
+    int ae = 0;
+    if (yf != 0.0f) {
+        if (yf > 0.5f) { yf -= 1.0f; yi += 1.0f; }
+        a1 = or_exp32(yf * or_log32(x));
+    }
+    int xe;
+    float x1 = frexpf(x, &xe);
+    for (int32_t i = (int32_t)yi; i != 0; i >>= 1) {
+        if (xe < -(1 << 9) || (1 << 9) < xe) { ae += xe; break; }
+        if (i & 1) { a1 *= x1; ae += xe; }
+        x1 *= x1;
+        xe <<= 1;
+        if (x1 < 0.5f) { x1 += x1; xe -= 1; }
+    }
+    if (y < 0.0f) { a1 = 1.0f / a1; ae = -ae; }
+    return ldexpf(a1, ae);
+}
 
 void or_params_default(or_params *p) {
     /* src/sampler.zig:3-27 defaults; the extension fields are neutral and the
@@ -154,13 +213,14 @@ uint32_t or_dry_edits(const uint32_t *hist, uint32_t n_hist, const uint32_t *bre
         }
     }
 #undef R
-    /* :178-186: penalty = mult * pow(base, min(rlen - allowed, max_exp)) */
-    float max_exp = (base > 1.0001f) ? 88.0f / logf(base) : 100.0f;
+    /* :178-186: penalty = mult * pow(base, min(rlen - allowed, max_exp)), with
+     * @log and std.math.pow as or_log32 / or_pow_zig */
+    float max_exp = (base > 1.0001f) ? 88.0f / or_log32(base) : 100.0f;
     for (uint32_t i = 0; i < n_pen; ++i) {
         float repeat_exp = (float)(pen_lens[i] - allowed);
         float e = repeat_exp < max_exp ? repeat_exp : max_exp;
         out_ids[i] = pen_toks[i];
-        out_deltas[i] = mult * powf(base, e);
+        out_deltas[i] = mult * or_pow_zig(base, e);
     }
     return n_pen;
 }

@@ -91,6 +91,8 @@ typedef struct or_sample_diag {
 } or_sample_diag;
 
 float or_exp32(float x);
+float or_log32(float x);
+float or_pow_zig(float x, float y);
 
 void or_params_default(or_params *p);
 

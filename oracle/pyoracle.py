@@ -101,6 +101,8 @@ def lib():
         L.or_softcap.argtypes = [C.c_float, C.c_float]
         L.or_exp32.restype = C.c_float
         L.or_exp32.argtypes = [C.c_float]
+        L.or_pow_zig.restype = C.c_float
+        L.or_pow_zig.argtypes = [C.c_float, C.c_float]
         L.or_params_default.argtypes = [C.POINTER(OrParams)]
         L.or_apply_penalty.argtypes = [f32p, C.c_uint32, u32p, C.c_uint32, C.c_float, C.c_float, C.c_float]
         L.or_apply_edits.argtypes = [f32p, C.c_uint32, u32p, f32p, C.c_uint32]
@@ -170,6 +172,10 @@ def softcap(x: float, cap: float) -> float:
 
 def exp32(x: float) -> float:
     return lib().or_exp32(float(x))
+
+
+def pow_zig(x: float, y: float) -> float:
+    return lib().or_pow_zig(float(x), float(y))
 
 
 def apply_penalty(logits: np.ndarray, window, rp: float, freq: float = 0.0, pres: float = 0.0) -> np.ndarray:

@@ -319,3 +319,37 @@ def test_softcap_precedes_mask_and_penalty(oracle, seed):
     pen_first = oracle.apply_penalty(x, win, 1.4)
     late = np.array([oracle.softcap(v, cap) for v in pen_first], np.float32)
     assert not np.array_equal(late[win], oracle.apply_penalty(capped, win, 1.4)[win])
+
+
+# ------------------------------------------------------------------ std.math.pow (DRY penalty)
+def test_pow_zig_special_cases(oracle):
+    """The special cases of std.math.pow, in its order: y = 0 or x = 1 give 1,
+    y = 1 gives x, y = +-0.5 take sqrt, 0 and infinities by sign rules."""
+    pw = oracle.pow_zig
+    assert pw(7.0, 0.0) == 1.0 and pw(1.0, 123.5) == 1.0 and pw(1.0, float("nan")) == 1.0
+    assert pw(1.75, 1.0) == np.float32(1.75)
+    assert pw(2.0, 0.5) == np.sqrt(np.float32(2.0)) and pw(2.0, -0.5) == np.float32(1) / np.sqrt(np.float32(2.0))
+    assert pw(0.0, 3.0) == 0.0 and pw(0.0, -2.0) == np.inf and np.signbit(pw(-0.0, 3.0))
+    assert pw(0.5, np.inf) == 0.0 and pw(2.0, np.inf) == np.inf and pw(-1.0, np.inf) == 1.0
+    assert pw(np.inf, -1.0) == 0.0 and pw(np.inf, 2.0) == np.inf
+    assert np.isnan(pw(-2.0, 0.5 + 0.25))
+
+
+@pytest.mark.parametrize("base", [1.75, 1.0001, 3.0, 1.1])
+def test_pow_zig_integer_and_fractional_powers(oracle, base):
+    """Integer exponents by repeated squaring and the fractional part through
+    exp(yf*log x): within the squaring chain's error bound of the f64 closed
+    form, about (2*yi + 16) f32 rounding errors relative (the error of
+    x1^(2^j) doubles with each squaring), where a dropped multiply, a wrong
+    exponent carry or an unshifted yf fails by far more; a single squaring
+    is exactly fl(x*x)."""
+    for y in list(range(0, 60)) + [0.3, 1.6, 2.75, 10.49, 10.51, 88.0 / np.log(np.float32(base))]:
+        yf = np.float32(y)
+        got = np.float64(oracle.pow_zig(base, float(yf)))
+        want = np.float64(np.float32(base)) ** np.float64(yf)
+        if not np.isfinite(want) or want > 3e38:
+            continue
+        tol = (2 * np.floor(abs(yf) + 0.5) + 16) * 2.0 ** -24 * want
+        assert abs(got - want) <= tol, (base, y, got, want)
+    b = np.float32(base)
+    assert oracle.pow_zig(base, 2.0) == np.float32(b * b)  # one squaring, one rounding

@@ -123,6 +123,9 @@ SIGNATURES = {
                                     C.POINTER(ZiSampleOut)]),
     "zi_sample_rows_pruned": (C.c_int32, [C.c_void_p, C.POINTER(ZiParams), C.POINTER(ZiBatch), C.c_void_p,
                                            C.c_void_p, C.c_int32, C.c_void_p, C.POINTER(ZiSampleOut)]),
+    "zi_dry_edits_rows": (C.c_int32, [C.c_void_p, C.POINTER(ZiParams), C.c_void_p, C.c_void_p, C.c_int32,
+                                       C.c_int32, C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p,
+                                       C.c_int32]),
     "zi_argmax_rows": (C.c_int32, [C.c_void_p, C.POINTER(ZiBatch), C.c_void_p, C.c_void_p, C.c_void_p,
                                     C.c_void_p]),
     "zi_entropy_topk_rows": (C.c_int32, [C.c_void_p, C.POINTER(ZiBatch), C.c_int32, C.c_void_p, C.c_void_p,

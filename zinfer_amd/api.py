@@ -121,6 +121,20 @@ class Context:
             check(lib().zi_sample_rows(self.h, C.byref(p), C.byref(b), _ptr(uniforms), C.byref(o)))
         return out
 
+    def dry_edits_rows(self, p: ZiParams, hist: torch.Tensor, hist_len: torch.Tensor,
+                       breakers: Optional[torch.Tensor] = None, edit_ld: int = 128):
+        """zi_dry_edits_rows: per-row DRY edits (ids [rows, edit_ld] int32,
+        deltas [rows, edit_ld] f32, counts [rows] int32) on the device."""
+        rows, dev = hist.shape[0], hist.device
+        ids = torch.zeros((rows, edit_ld), dtype=torch.int32, device=dev)
+        delta = torch.zeros((rows, edit_ld), dtype=torch.float32, device=dev)
+        cnt = torch.empty(rows, dtype=torch.int32, device=dev)
+        nb = 0 if breakers is None else int(breakers.numel())
+        self._bind_stream()
+        check(lib().zi_dry_edits_rows(self.h, C.byref(p), _ptr(hist), _ptr(hist_len), hist.stride(0), rows,
+                                      _ptr(breakers), nb, _ptr(ids), _ptr(delta), _ptr(cnt), edit_ld))
+        return ids, delta, cnt
+
     def argmax_rows(self, logits: torch.Tensor, vocab=None):
         rows, dev = logits.shape[0], logits.device
         tok = torch.empty(rows, dtype=torch.int32, device=dev)

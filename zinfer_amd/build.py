@@ -17,7 +17,7 @@ CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libzinfer_hip.so")
 OBJ = os.path.join(ROOT, "_build", "obj")
 
-SOURCES = ["zi_sample.hip", "zi_sample_cap.hip", "zi_exact.hip", "zi_argmax.hip", "zi_entropy.hip", "zi_grammar.hip", "zi_pruned.hip",
+SOURCES = ["zi_sample.hip", "zi_sample_cap.hip", "zi_exact.hip", "zi_argmax.hip", "zi_entropy.hip", "zi_grammar.hip", "zi_pruned.hip", "zi_dry.hip",
            "zi_api.cpp",
            "zi_host.cpp"]
 

@@ -14,6 +14,7 @@
 #include "../../include/zinfer_hip.h"
 #include "zi_internal.hpp"
 #include "zi_launch.hpp"
+#include "zi_pow.hpp"
 
 namespace {
 
@@ -165,11 +166,8 @@ uint32_t zi_dry_edits_impl(const uint32_t *hist, uint32_t n_hist, const uint32_t
             ++n_pen;
         }
     }
-    const float max_exp = (p.dry_base > 1.0001f) ? 88.0f / std::log(p.dry_base) : 100.0f;
-    for (uint32_t i = 0; i < n_pen; ++i) {
-        float e = std::min((float)(lens[i] - p.dry_allowed_length), max_exp);
-        out_deltas[i] = p.dry_multiplier * std::pow(p.dry_base, e);
-    }
+    for (uint32_t i = 0; i < n_pen; ++i)
+        out_deltas[i] = zi::dry_penalty(lens[i], p.dry_multiplier, p.dry_base, p.dry_allowed_length);
     return n_pen;
 }
 
