@@ -21,6 +21,10 @@
  *                          crafted windows.
  *   or_dry_edits           pinned: reference KAT sampler.zig:634-673 (9.2, 8.4,
  *                          breaker keeps 10.0) and brute-force longest-suffix match.
+ *   or_pow_zig             std.math.pow restated (Go math.Pow algorithm): special
+ *                          cases, integer powers within the repeated-squaring
+ *                          bound of the f64 closed form, the fractional split;
+ *                          last-ulp agreement with Zig PARITY UNPINNED (no Zig).
  *   or_sample              pinned: KATs sampler.zig:675-702 (min-p) and :704-748
  *                          (XTC); top-k order vs numpy lexsort; top-p keep vs numpy
  *                          float32 add.accumulate; draw vs inverse-CDF on
