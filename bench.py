@@ -36,6 +36,8 @@ def parse():
     ap.add_argument("--path", choices=["sample", "json_mask", "verify", "dry"], default="sample",
                     help="sample: zi_sample_rows on --config (the headline); json_mask: zi_json_mask_rows; "
                          "verify: zi_sampler_verify")
+    ap.add_argument("--branches", type=int, default=1,
+                    help="verify path: > 1 verifies that many 8-token branches in one call (zi_sampler_verify_tree)")
     ap.add_argument("--softcap", type=float, default=0.0,
                     help="final-logit softcap fused into the read (sample path; 0 = off, the config's default)")
     ap.add_argument("--pruned", type=int, default=0,
@@ -189,27 +191,39 @@ def bench_verify(args):
     from zinfer_amd.api import Context, Sampler, params
 
     V, k = 151936, 8
+    nbr = max(1, args.branches)
     rng = np.random.Generator(np.random.PCG64(808))
-    X = (rng.standard_normal((k + 1, V)) * 2.5).astype(np.float32)
-    draft = [int(t) for t in rng.integers(0, V, k)]
-    for i, t in enumerate(draft):
-        X[i, t] += 25.0  # the target agrees with the draft (well above the row maximum)
+    Xb, drafts = [], []
+    for j in range(nbr):  # branch j: the target agrees with its draft up to token 8 - 2j
+        Xj = (rng.standard_normal((k + 1, V)) * 2.5).astype(np.float32)
+        dj = [int(t) for t in rng.integers(0, V, k)]
+        for i, t in enumerate(dj[:max(0, k - 2 * j)]):
+            Xj[i, t] += 25.0  # well above the row maximum
+        Xb.append(Xj)
+        drafts.append(dj)
+    X, draft = Xb[0], drafts[0]
     pk = dict(temp=0.8, top_k=40, top_p=0.95, min_p=0.05, repeat_penalty=1.1, penalty_last_n=64, seed=9)
     hist = [int(t) for t in rng.integers(0, V, 64)]
-    ctx = Context(0, max_rows=16, max_vocab=V)
+    ctx = Context(0, max_rows=max(16, nbr * (k + 1)), max_vocab=V)
     dev = torch.device("cuda:0")
-    L = torch.from_numpy(X).to(dev)
+    L = torch.from_numpy(np.concatenate(Xb) if nbr > 1 else X).to(dev)
     smp = Sampler(ctx, V, params(**pk))
     for t in hist:
         smp.accept(t)
+
+    def call():
+        if nbr > 1:
+            return max(smp.verify_tree(L, drafts, commit=False)[0])
+        return smp.verify(L, draft)[0]
+
     for _ in range(max(1, args.warmup // 16)):
-        smp.verify(L, draft)
+        call()
     torch.cuda.synchronize()
     steps = max(16, args.steps)
     accepted = []
     t0 = time.perf_counter()
     for _ in range(steps):
-        accepted.append(smp.verify(L, draft)[0])
+        accepted.append(call())
     wall = time.perf_counter() - t0
     ms = wall * 1e3 / steps
     # one call per row through the host-row sampler, for contrast
@@ -219,8 +233,9 @@ def bench_verify(args):
     reps = max(4, steps // 8)
     t1 = time.perf_counter()
     for _ in range(reps):
-        for i in range(k + 1):
-            seq.sample_with_margin(X[i].copy())
+        for Xj in Xb:
+            for i in range(k + 1):
+                seq.sample_with_margin(Xj[i].copy())
     ms_seq = (time.perf_counter() - t1) * 1e3 / reps
 
     from oracle import pyoracle
@@ -231,28 +246,32 @@ def bench_verify(args):
     if args.cpu_seconds > 0:
         n_cpu, tc0 = 0, time.perf_counter()
         while time.perf_counter() - tc0 < min(args.cpu_seconds, 10.0):
-            h, pos = list(hist), 0
-            for i in range(k + 1):
-                tok, _, d = pyoracle.sample_row(op, X[i], stream[pos:pos + 2], window=np.array(h[-64:], np.uint32))
-                pos += d["ndraws"]
-                if i < k and tok == draft[i]:
-                    h.append(tok)
-                    continue
-                break
+            for Xj, dj in zip(Xb, drafts):  # one sequential loop per branch
+                h, pos = list(hist), 0
+                for i in range(k + 1):
+                    tok, _, d = pyoracle.sample_row(op, Xj[i], stream[pos:pos + 2],
+                                                    window=np.array(h[-64:], np.uint32))
+                    pos += d["ndraws"]
+                    if i < k and tok == dj[i]:
+                        h.append(tok)
+                        continue
+                    break
             n_cpu += 1
         tc = time.perf_counter() - tc0
         cpu = {"value": round(n_cpu / tc, 2), "unit": "verify calls/s", "cores": 1, "kind": "port",
-               "sample": f"{n_cpu} sequential verify loops of {k} drafted tokens + bonus row ({tc:.1f} s), "
+               "sample": f"{n_cpu} x {nbr} sequential verify loops of {k} drafted tokens + bonus row ({tc:.1f} s), "
                          f"oracle/oracle.c sample_row (C restatement of src/sampler.zig:190-276), 1 thread"}
-    nbytes = (k + 1) * V * 4
+    nbytes = nbr * (k + 1) * V * 4
     achieved = nbytes / (ms * 1e-3) / 1e9
+    entry = "zi_sampler_verify_tree, %d branches of" % nbr if nbr > 1 else "zi_sampler_verify,"
     print(json.dumps({
-        "metric": "draft verification calls/sec (zi_sampler_verify, 8 drafted tokens + bonus row, V=151936 f32)",
+        "metric": f"draft verification calls/sec ({entry} 8 drafted tokens + bonus row, V=151936 f32)",
         "value": round(1e3 / ms, 1), "unit": "verify calls/s", "n_gpus": 1, "steps": steps,
         "warmup": max(1, args.warmup // 16), "ms_per_step": round(ms, 6), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic, seeded (bench.py bench_verify): N(0, 2.5^2) rows, draft tokens +25",
-        "config": {"workload": "verify_k8_151936_f32", "drafted": k, "vocab": V, **pk,
+        "config": {"workload": f"verify_{nbr}x8_151936_f32" if nbr > 1 else "verify_k8_151936_f32", "drafted": k,
+                   "branches": nbr, "vocab": V, **pk,
                    "accepted_mean": float(np.mean(accepted)), "one_call_per_row_ms": round(ms_seq, 4),
                    "timing": "host wall clock per synchronous call"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",

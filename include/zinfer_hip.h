@@ -280,6 +280,25 @@ int32_t zi_sampler_verify(zi_sampler *s, const zi_batch *b, const uint32_t *draf
                           uint32_t max_accept, const uint32_t *eog, uint32_t n_eog, zi_vocab *v,
                           zi_json_state *json, uint32_t *out_accepted, uint32_t *out_next,
                           float *out_margin);
+
+/* Tree verification (the batched tree verify of the reference's roadmap,
+ * ROADMAP.md:134-135, over CandidateTree branches, src/sampler.zig:291-475):
+ * n_branches (<= 8) drafts, branch j = drafts[j * draft_ld .. + ks[j]]
+ * (ks[j] <= 16), verified in one zi_sample_rows launch.  b holds branch j's
+ * rows at base_j .. base_j + ks[j], base_j = sum over i < j of (ks[i] + 1),
+ * each row as zi_sampler_verify reads it.  Branch j's results are exactly what
+ * zi_sampler_verify would return for that draft alone from the sampler's
+ * current state (every branch starts at the same RNG draw).  out_accepted /
+ * out_next / out_margin [n_branches]; *out_best = the branch with the most
+ * accepted tokens (the first on ties).  With commit != 0 the sampler and
+ * *json are left as zi_sampler_verify on that branch leaves them; with 0 they
+ * are untouched.  Synchronous. */
+int32_t zi_sampler_verify_tree(zi_sampler *s, const zi_batch *b, const uint32_t *drafts,
+                               uint32_t draft_ld, const uint32_t *ks, uint32_t n_branches,
+                               uint32_t max_accept, const uint32_t *eog, uint32_t n_eog,
+                               zi_vocab *v, zi_json_state *json, int32_t commit,
+                               uint32_t *out_accepted, uint32_t *out_next, float *out_margin,
+                               uint32_t *out_best);
 /* Read / replace the params (server.zig:377-415 writes g.smp.p fields). */
 void    zi_sampler_get_params(const zi_sampler *s, zi_params *p);
 void    zi_sampler_set_params(zi_sampler *s, const zi_params *p);

@@ -152,6 +152,9 @@ SIGNATURES = {
     "zi_sampler_sample": (C.c_int32, [C.c_void_p, f32p, C.c_uint32, u32p]),
     "zi_sampler_verify": (C.c_int32, [C.c_void_p, C.POINTER(ZiBatch), u32p, C.c_uint32, C.c_uint32, u32p, C.c_uint32,
                                        C.c_void_p, jsp, u32p, u32p, f32p]),
+    "zi_sampler_verify_tree": (C.c_int32, [C.c_void_p, C.POINTER(ZiBatch), u32p, C.c_uint32, u32p, C.c_uint32,
+                                            C.c_uint32, u32p, C.c_uint32, C.c_void_p, C.c_void_p, C.c_int32, u32p,
+                                            u32p, f32p, u32p]),
     "zi_sampler_get_params": (None, [C.c_void_p, C.POINTER(ZiParams)]),
     "zi_sampler_set_params": (None, [C.c_void_p, C.POINTER(ZiParams)]),
     "zi_sampler_seed": (None, [C.c_void_p, C.c_uint64]),

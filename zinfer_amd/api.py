@@ -238,6 +238,35 @@ class Sampler:
                                       C.byref(a), C.byref(nt), C.byref(m)))
         return int(a.value), int(nt.value), float(m.value)
 
+    def verify_tree(self, logits: torch.Tensor, drafts, *, max_accept: int = 2**32 - 1, eog=(), vocab=None,
+                    json: Optional["JsonValidator"] = None, commit: bool = True):
+        """Tree verification (zi_sampler_verify_tree): `drafts` is a list of
+        branches; logits holds each branch's len + 1 rows back to back.
+        Returns (accepted[], next[], margin[], best)."""
+        import numpy as np
+        nb = len(drafts)
+        ld = max(1, max(len(d) for d in drafts))
+        D = np.zeros((nb, ld), np.uint32)
+        ks = np.zeros(nb, np.uint32)
+        for j, d in enumerate(drafts):
+            D[j, :len(d)] = np.asarray(d, dtype=np.uint32)
+            ks[j] = len(d)
+        e = np.ascontiguousarray(np.asarray(eog, dtype=np.uint32).reshape(-1))
+        b = Context.batch(logits, self.vocab)
+        acc = np.zeros(nb, np.uint32)
+        nxt = np.zeros(nb, np.uint32)
+        mg = np.zeros(nb, np.float32)
+        best = C.c_uint32()
+        self.ctx._bind_stream()
+        check(lib().zi_sampler_verify_tree(self.h, C.byref(b), D.ctypes.data_as(_lib.u32p), ld,
+                                           ks.ctypes.data_as(_lib.u32p), nb, max_accept,
+                                           e.ctypes.data_as(_lib.u32p) if e.size else None, e.size,
+                                           vocab.h if vocab is not None else None,
+                                           C.byref(json.st) if json is not None else None, 1 if commit else 0,
+                                           acc.ctypes.data_as(_lib.u32p), nxt.ctypes.data_as(_lib.u32p),
+                                           mg.ctypes.data_as(_lib.f32p), C.byref(best)))
+        return [int(a) for a in acc], [int(t) for t in nxt], [float(m) for m in mg], int(best.value)
+
     def get_params(self) -> ZiParams:
         p = ZiParams()
         lib().zi_sampler_get_params(self.h, C.byref(p))

@@ -374,42 +374,59 @@ extern "C" int32_t zi_sampler_sample_with_margin(zi_sampler *s, float *logits, u
 // row's uniforms at its offset in the stream.
 constexpr uint32_t kMaxVerify = 16;  // drafted tokens per call (the reference drafts at most 8)
 
-extern "C" int32_t zi_sampler_verify(zi_sampler *s, const zi_batch *b, const uint32_t *draft, uint32_t k,
-                                     uint32_t max_accept, const uint32_t *eog, uint32_t n_eog, zi_vocab *v,
-                                     zi_json_state *json, uint32_t *out_accepted, uint32_t *out_next,
-                                     float *out_margin) {
-    if (!s || !b || !b->logits || (k && !draft) || (n_eog && !eog) || !out_accepted || !out_next)
-        return zi_fail(ZI_ERR_INVALID, "zi_sampler_verify: bad argument");
-    if (k > kMaxVerify) return zi_fail(ZI_ERR_UNSUPPORTED, "zi_sampler_verify: k=%u > %u", k, kMaxVerify);
-    if ((uint32_t)b->vocab != s->vocab || b->rows < (int32_t)k + 1)
-        return zi_fail(ZI_ERR_INVALID, "zi_sampler_verify: batch of %d x %d for k=%u, vocab %u", b->rows, b->vocab, k,
-                       s->vocab);
-    if ((v == nullptr) != (json == nullptr))
-        return zi_fail(ZI_ERR_INVALID, "zi_sampler_verify: vocab and json state go together");
+constexpr uint32_t kMaxBranches = 8;  // branches per tree verify (the reference's tree holds 4, sampler.zig:291)
+constexpr uint32_t kMaxVerifyRows = kMaxBranches * (kMaxVerify + 1);
+
+// Verification of nbr drafts (branches) from the sampler's current state in
+// one zi_sample_rows launch: branch j's rows are b's rows base_j .. base_j +
+// k_j, base_j = sum of (k_i + 1) over i < j, each sampled as the reference's
+// loop would sample it were branch j verified alone.  With commit, the branch
+// with the most accepted tokens (the first on ties) is applied to the sampler
+// and *json; *out_best names it.
+static int32_t verify_core(zi_sampler *s, const zi_batch *b, const uint32_t *const *drafts, const uint32_t *ks,
+                           uint32_t nbr, uint32_t max_accept, const uint32_t *eog, uint32_t n_eog, zi_vocab *v,
+                           zi_json_state *json, bool commit, uint32_t *out_accepted, uint32_t *out_next,
+                           float *out_margin, uint32_t *out_best, const char *fn) {
+    if (!s || !b || !b->logits || !ks || nbr == 0 || (n_eog && !eog) || !out_accepted || !out_next)
+        return zi_fail(ZI_ERR_INVALID, "%s: bad argument", fn);
+    if (nbr > kMaxBranches) return zi_fail(ZI_ERR_UNSUPPORTED, "%s: %u branches > %u", fn, nbr, kMaxBranches);
+    uint32_t base[kMaxBranches + 1];
+    base[0] = 0;
+    for (uint32_t j = 0; j < nbr; ++j) {
+        if (ks[j] > kMaxVerify) return zi_fail(ZI_ERR_UNSUPPORTED, "%s: k=%u > %u", fn, ks[j], kMaxVerify);
+        if (ks[j] && !drafts[j]) return zi_fail(ZI_ERR_INVALID, "%s: branch %u has no draft", fn, j);
+        base[j + 1] = base[j] + ks[j] + 1;
+    }
+    const uint32_t R = base[nbr];
+    if ((uint32_t)b->vocab != s->vocab || b->rows < (int32_t)R)
+        return zi_fail(ZI_ERR_INVALID, "%s: batch of %d x %d for %u rows, vocab %u", fn, b->rows, b->vocab, R, s->vocab);
+    if ((v == nullptr) != (json == nullptr)) return zi_fail(ZI_ERR_INVALID, "%s: vocab and json state go together", fn);
     if (v && zi_vocab_size(v) != (int32_t)s->vocab)
-        return zi_fail(ZI_ERR_INVALID, "zi_sampler_verify: vocab has %d tokens, sampler %u", zi_vocab_size(v), s->vocab);
+        return zi_fail(ZI_ERR_INVALID, "%s: vocab has %d tokens, sampler %u", fn, zi_vocab_size(v), s->vocab);
     zi_ctx *c = s->ctx;
-    const uint32_t R = k + 1;
-    if ((int32_t)R > c->max_rows) return zi_fail(ZI_ERR_CAPACITY, "zi_sampler_verify: %u rows > max_rows", R);
+    if ((int32_t)R > c->max_rows) return zi_fail(ZI_ERR_CAPACITY, "%s: %u rows > max_rows", fn, R);
     const zi_params &p = s->p;
     if (p.penalty_last_n > (uint32_t)zi::kMaxWinHost)
         return zi_fail(ZI_ERR_UNSUPPORTED, "penalty_last_n %u > %d", p.penalty_last_n, zi::kMaxWinHost);
     const uint32_t W = (s->vocab + 31) / 32;
-    const uint32_t RM = kMaxVerify + 1;
+    const uint32_t RM = R;
+    // window rows only as wide as the window, so the copy to the device stays small
+    const uint32_t WP = std::max<uint32_t>(1u, std::min<uint32_t>(p.penalty_last_n, (uint32_t)zi::kMaxWinHost));
     size_t o = 0;
-    const size_t o_hist = o;
-    o = align_up(o + (size_t)RM * zi::kMaxWinHost * 4, 256);
+    const size_t o_u = o;
+    o = align_up(o + RM * 8, 256);
     const size_t o_hlen = o;
     o = align_up(o + RM * 4, 256);
+    const size_t o_hist = o;
+    o = align_up(o + (size_t)RM * WP * 4, 256);
+    const size_t o_in = o;  // host -> device up to here on every pass
     const size_t o_eids = o;
     o = align_up(o + (size_t)RM * zi::kMaxEditsHost * 4, 256);
     const size_t o_edel = o;
     o = align_up(o + (size_t)RM * zi::kMaxEditsHost * 4, 256);
     const size_t o_ecnt = o;
     o = align_up(o + RM * 4, 256);
-    const size_t o_u = o;
-    o = align_up(o + RM * 8, 256);
-    const size_t o_in = o;  // host -> device up to here
+    const size_t o_in_edits = o;  // ... and up to here when there are DRY edits
     const size_t o_tok = o;
     o = align_up(o + RM * 4, 256);
     const size_t o_margin = o;
@@ -420,61 +437,67 @@ extern "C" int32_t zi_sampler_verify(zi_sampler *s, const zi_batch *b, const uin
     const size_t o_mask = o;
     o = align_up(o + (size_t)RM * W * 4, 256);
     hipError_t e = hipSetDevice(c->device);
-    if (e != hipSuccess) return zi_hip_fail(e, "zi_sampler_verify: hipSetDevice");
+    if (e != hipSuccess) return zi_hip_fail(e, "verify: hipSetDevice");
     int32_t rc = s->vst.ensure(o);
     if (rc) return rc;
     char *h = (char *)s->vst.h;
     char *d = (char *)s->vst.d;
 
-    // per-row penalty windows and DRY edits: the history plus draft[0..i)
-    uint32_t lin[kMaxHistory + kMaxVerify];
+    // per-row penalty windows and DRY edits: the history plus the branch's draft[0..i)
+    static thread_local uint32_t lin[kMaxHistory + kMaxVerify];
     const uint32_t nlin = s->window(kMaxHistory, lin);
-    std::memcpy(lin + nlin, draft, (size_t)k * 4);
     bool any_edits = false;
-    for (uint32_t i = 0; i < R; ++i) {
-        const uint32_t len = nlin + i;
-        const uint32_t nw = std::min<uint32_t>(len, p.penalty_last_n);
-        std::memcpy(h + o_hist + (size_t)i * zi::kMaxWinHost * 4, lin + len - nw, (size_t)nw * 4);
-        ((int32_t *)(h + o_hlen))[i] = (int32_t)nw;
-        uint32_t ne = 0;
-        if (p.dry_multiplier != 0.0f) {
-            const uint32_t hl = std::min<uint32_t>(len, kMaxHistory);
-            ne = zi_dry_edits_impl(lin + len - hl, hl, s->breakers, s->n_breakers, p,
-                                   (uint32_t *)(h + o_eids) + (size_t)i * zi::kMaxEditsHost,
-                                   (float *)(h + o_edel) + (size_t)i * zi::kMaxEditsHost);
+    for (uint32_t j = 0; j < nbr; ++j) {
+        std::memcpy(lin + nlin, drafts[j], (size_t)ks[j] * 4);
+        for (uint32_t i = 0; i <= ks[j]; ++i) {
+            const uint32_t row = base[j] + i;
+            const uint32_t len = nlin + i;
+            const uint32_t nw = std::min<uint32_t>(len, std::min<uint32_t>(p.penalty_last_n, WP));
+            std::memcpy(h + o_hist + (size_t)row * WP * 4, lin + len - nw, (size_t)nw * 4);
+            ((int32_t *)(h + o_hlen))[row] = (int32_t)nw;
+            uint32_t ne = 0;
+            if (p.dry_multiplier != 0.0f) {
+                const uint32_t hl = std::min<uint32_t>(len, kMaxHistory);
+                ne = zi_dry_edits_impl(lin + len - hl, hl, s->breakers, s->n_breakers, p,
+                                       (uint32_t *)(h + o_eids) + (size_t)row * zi::kMaxEditsHost,
+                                       (float *)(h + o_edel) + (size_t)row * zi::kMaxEditsHost);
+            }
+            ((int32_t *)(h + o_ecnt))[row] = (int32_t)ne;
+            any_edits |= ne > 0;
         }
-        ((int32_t *)(h + o_ecnt))[i] = (int32_t)ne;
-        any_edits |= ne > 0;
     }
-    // per-row JSON states: the validator after consuming draft[0..i)
-    zi_json_state states[kMaxVerify + 1];
+    // per-row JSON states: the validator after consuming the branch's draft[0..i)
+    static thread_local zi_json_state states[kMaxVerifyRows];
     if (v) {
-        zi_json_state st = *json;
-        for (uint32_t i = 0; i < R; ++i) {
-            states[i] = st;
-            if (i < k) {
-                const uint8_t *pc;
-                uint32_t pn;
-                if (!zi_vocab_piece(v, draft[i], &pc, &pn))
-                    return zi_fail(ZI_ERR_INVALID, "zi_sampler_verify: draft token %u out of range", draft[i]);
-                zi_json_consume(&st, pc, pn);
+        for (uint32_t j = 0; j < nbr; ++j) {
+            zi_json_state st = *json;
+            for (uint32_t i = 0; i <= ks[j]; ++i) {
+                states[base[j] + i] = st;
+                if (i < ks[j]) {
+                    const uint8_t *pc;
+                    uint32_t pn;
+                    if (!zi_vocab_piece(v, drafts[j][i], &pc, &pn))
+                        return zi_fail(ZI_ERR_INVALID, "%s: draft token %u out of range", fn, drafts[j][i]);
+                    zi_json_consume(&st, pc, pn);
+                }
             }
         }
     }
-    // draws: row i takes its uniforms at offset off[i] of the stream
+    // draws: every branch starts at the sampler's next draw; row i of a
+    // branch takes its uniforms at offset off[i] of that stream
     Xoshiro peek = s->rng;
     float stream[2 * (kMaxVerify + 1) + 2];
-    for (uint32_t i = 0; i < 2 * R + 2; ++i) stream[i] = peek.f32();
+    for (uint32_t i = 0; i < 2 * (kMaxVerify + 1) + 2; ++i) stream[i] = peek.f32();
     const bool sampled = p.temp > 0.0f;
     const bool xtc = sampled && p.xtc_probability > 0.0f && p.xtc_threshold <= 0.5f;
-    int32_t nd[kMaxVerify + 1];
+    static thread_local int32_t nd[kMaxVerifyRows];
     for (uint32_t i = 0; i < R; ++i) nd[i] = sampled ? 1 : 0;
 
     zi_batch bb = *b;
     bb.rows = (int32_t)R;
     bb.hist = (const uint32_t *)(d + o_hist);
     bb.hist_len = (const int32_t *)(d + o_hlen);
-    bb.hist_ld = zi::kMaxWinHost;
+    bb.hist_ld = (int32_t)WP;
     bb.mask = v ? (const uint32_t *)(d + o_mask) : nullptr;
     bb.mask_ld = (int32_t)W;
     bb.edit_ids = any_edits ? (const uint32_t *)(d + o_eids) : nullptr;
@@ -492,43 +515,82 @@ extern "C" int32_t zi_sampler_verify(zi_sampler *s, const zi_batch *b, const uin
     }
     for (int pass = xtc ? 0 : 1; pass < 2; ++pass) {
         float *u = (float *)(h + o_u);
-        uint32_t off = 0;
-        for (uint32_t i = 0; i < R; ++i) {
-            u[2 * i] = stream[off];
-            u[2 * i + 1] = stream[off + 1];
-            off += (uint32_t)nd[i];
+        for (uint32_t j = 0; j < nbr; ++j) {
+            uint32_t off = 0;
+            for (uint32_t i = base[j]; i < base[j + 1]; ++i) {
+                u[2 * i] = stream[off];
+                u[2 * i + 1] = stream[off + 1];
+                off += (uint32_t)nd[i];
+            }
         }
-        e = hipMemcpyAsync(d, h, o_in, hipMemcpyHostToDevice, c->stream);
-        if (e != hipSuccess) return zi_hip_fail(e, "zi_sampler_verify: H2D");
+        e = hipMemcpyAsync(d, h, any_edits && pass == (xtc ? 0 : 1) ? o_in_edits : o_in, hipMemcpyHostToDevice,
+                           c->stream);
+        if (e != hipSuccess) return zi_hip_fail(e, "verify: H2D");
         rc = zi_sample_rows(c, &p, &bb, (const float *)(d + o_u), &so);
         if (rc) return rc;
         e = hipMemcpyAsync(h + o_tok, d + o_tok, o_out - o_tok, hipMemcpyDeviceToHost, c->stream);
         if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-        if (e != hipSuccess) return zi_hip_fail(e, "zi_sampler_verify: D2H");
+        if (e != hipSuccess) return zi_hip_fail(e, "verify: D2H");
         for (uint32_t i = 0; i < R; ++i) nd[i] = ((const int32_t *)(h + o_nd))[i];
     }
     const uint32_t *tok = (const uint32_t *)(h + o_tok);
     const float *mg = (const float *)(h + o_margin);
-    uint32_t a = 0;
-    while (a < k && a < max_accept && tok[a] == draft[a] && std::find(eog, eog + n_eog, tok[a]) == eog + n_eog) ++a;
-    // side effects of the reference loop: take() for the accepted tokens, and
-    // the draws of rows 0..a (the rows it sampled)
+    uint32_t best = 0;
+    for (uint32_t j = 0; j < nbr; ++j) {
+        const uint32_t *t = tok + base[j];
+        const uint32_t *dr = drafts[j];
+        uint32_t a = 0;
+        while (a < ks[j] && a < max_accept && t[a] == dr[a] && std::find(eog, eog + n_eog, t[a]) == eog + n_eog) ++a;
+        out_accepted[j] = a;
+        out_next[j] = t[a];
+        if (out_margin) out_margin[j] = mg[base[j] + a];
+        if (a > out_accepted[best]) best = j;
+    }
+    if (out_best) *out_best = best;
+    if (!commit) return ZI_OK;
+    // side effects of the reference loop for the chosen branch: take() for the
+    // accepted tokens, and the draws of rows 0..a (the rows it sampled)
+    const uint32_t a = out_accepted[best];
     uint32_t used = 0;
-    for (uint32_t i = 0; i <= a; ++i) used += (uint32_t)nd[i];
+    for (uint32_t i = 0; i <= a; ++i) used += (uint32_t)nd[base[best] + i];
     for (uint32_t i = 0; i < used; ++i) (void)s->rng.f32();
     for (uint32_t i = 0; i < a; ++i) {
-        zi_sampler_accept(s, draft[i]);
+        zi_sampler_accept(s, drafts[best][i]);
         if (v) {
             const uint8_t *pc;
             uint32_t pn;
-            zi_vocab_piece(v, draft[i], &pc, &pn);
+            zi_vocab_piece(v, drafts[best][i], &pc, &pn);
             zi_json_consume(json, pc, pn);
         }
     }
-    *out_accepted = a;
-    *out_next = tok[a];
-    if (out_margin) *out_margin = mg[a];
     return ZI_OK;
+}
+
+extern "C" int32_t zi_sampler_verify(zi_sampler *s, const zi_batch *b, const uint32_t *draft, uint32_t k,
+                                     uint32_t max_accept, const uint32_t *eog, uint32_t n_eog, zi_vocab *v,
+                                     zi_json_state *json, uint32_t *out_accepted, uint32_t *out_next,
+                                     float *out_margin) {
+    if (k && !draft) return zi_fail(ZI_ERR_INVALID, "zi_sampler_verify: bad argument");
+    const uint32_t *drafts[1] = {draft};
+    return verify_core(s, b, drafts, &k, 1, max_accept, eog, n_eog, v, json, true, out_accepted, out_next,
+                       out_margin, nullptr, "zi_sampler_verify");
+}
+
+extern "C" int32_t zi_sampler_verify_tree(zi_sampler *s, const zi_batch *b, const uint32_t *drafts, uint32_t draft_ld,
+                                          const uint32_t *ks, uint32_t n_branches, uint32_t max_accept,
+                                          const uint32_t *eog, uint32_t n_eog, zi_vocab *v, zi_json_state *json,
+                                          int32_t commit, uint32_t *out_accepted, uint32_t *out_next,
+                                          float *out_margin, uint32_t *out_best) {
+    if (!drafts || !ks || n_branches == 0 || n_branches > kMaxBranches)
+        return zi_fail(n_branches > kMaxBranches ? ZI_ERR_UNSUPPORTED : ZI_ERR_INVALID,
+                       "zi_sampler_verify_tree: %u branches (1..%u) or NULL drafts", n_branches, kMaxBranches);
+    const uint32_t *rows[kMaxBranches];
+    for (uint32_t j = 0; j < n_branches; ++j) {
+        if (ks[j] > draft_ld) return zi_fail(ZI_ERR_INVALID, "zi_sampler_verify_tree: k=%u > draft_ld", ks[j]);
+        rows[j] = drafts + (size_t)j * draft_ld;
+    }
+    return verify_core(s, b, rows, ks, n_branches, max_accept, eog, n_eog, v, json, commit != 0, out_accepted,
+                       out_next, out_margin, out_best, "zi_sampler_verify_tree");
 }
 
 extern "C" int32_t zi_sampler_sample(zi_sampler *s, float *logits, uint32_t n, uint32_t *tok) {
