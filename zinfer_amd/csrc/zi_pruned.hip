@@ -124,10 +124,31 @@ __global__ __launch_bounds__(kThreads) void pruned_kernel(SampleParams P) {
     const uint32_t V = (uint32_t)a.V;
     const uint32_t ngt = (V + 7) / 8;  // groups of the vocabulary
 
+    // Every load that does not need a group id goes out first, together with
+    // the ids and their count (the id slots up to groups_ld, not up to the
+    // count, so that the ids do not wait for it): one round trip; then the
+    // logits, which need the ids.
     PenRegs pr;
-    if (HAS_PEN) pen_prefetch(a, row, pr);
+    int hl_raw = 0, ne_raw = 0;
+    if (HAS_PEN) {
+        pen_prefetch(a, row, pr);
+        int rr = row;
+        asm volatile("" : "+v"(rr));  // vector loads: their waits are counted with the others
+        if (row_pen_window_on(a)) hl_raw = a.hist_len[rr];
+        if (a.edit_ids) ne_raw = a.edit_count[rr];
+    }
+    int ur = 2 * row;
+    asm volatile("" : "+v"(ur));
+    const float u0 = P.uniforms ? P.uniforms[ur] : 0.0f, u1 = P.uniforms ? P.uniforms[ur + 1] : 0.0f;
+    const int gcap = min(P.groups_ld, kMaxGroups);
+    uint32_t graw[kGroupsPerThread];
+#pragma unroll
+    for (int u = 0; u < kGroupsPerThread; ++u) {
+        const int j = tid + u * kThreads;
+        graw[u] = j < gcap ? P.groups[(int64_t)row * P.groups_ld + j] : kNoGroup;
+    }
     int ng = P.group_count[row];
-    ng = ng < 0 ? 0 : min(ng, min(P.groups_ld, kMaxGroups));
+    ng = ng < 0 ? 0 : min(ng, gcap);
     uint32_t gid[kGroupsPerThread];
     const T *base = reinterpret_cast<const T *>(a.logits) + (int64_t)row * a.ld;
     uint4 raw[kGroupsPerThread][NL];
@@ -135,7 +156,7 @@ __global__ __launch_bounds__(kThreads) void pruned_kernel(SampleParams P) {
 #pragma unroll
     for (int u = 0; u < kGroupsPerThread; ++u) {
         const int j = tid + u * kThreads;
-        uint32_t g = j < ng ? P.groups[(int64_t)row * P.groups_ld + j] : kNoGroup;
+        uint32_t g = j < ng ? graw[u] : kNoGroup;
         g = g < ngt ? g : kNoGroup;
         gid[u] = g;
         const uint32_t gl = g == kNoGroup ? 0u : g;  // loads stay in the row either way
@@ -143,14 +164,11 @@ __global__ __launch_bounds__(kThreads) void pruned_kernel(SampleParams P) {
         for (int q = 0; q < NL; ++q) raw[u][q] = *reinterpret_cast<const uint4 *>(base + gl * 8u + q * VEC);
         mw[u] = HAS_MASK ? a.mask[(int64_t)row * a.mask_ld + ((gl * 8u) >> 5)] : 0xFFFFFFFFu;
     }
-    int ur = 2 * row;
-    asm volatile("" : "+v"(ur));
-    const float u0 = P.uniforms ? P.uniforms[ur] : 0.0f, u1 = P.uniforms ? P.uniforms[ur + 1] : 0.0f;
 
     for (int i = tid; i < (int)((ngt + 31) / 32); i += kThreads) s.gbits[i] = 0u;
     RowPen rp;
     if (HAS_PEN) {
-        rp = row_pen(a, row);
+        rp = row_pen_from(a, row, hl_raw, ne_raw);
         pen_window(rp, pr);
         for (int i = tid; i < (1 << rp.hs_log2); i += kThreads) {
             s.key[i] = 0u;

@@ -99,13 +99,19 @@ struct RowPen {
     bool any;
 };
 
-__device__ __forceinline__ RowPen row_pen(const RowSource &a, int row) {
+// hl_raw / ne_raw: hist_len[row] / edit_count[row] as loaded (callers that
+// issue those loads early pass them in; row_pen loads them itself).
+__device__ __forceinline__ bool row_pen_window_on(const RowSource &a) {
+    return a.hist && (a.do_rep || a.do_fp) && a.win > 0;
+}
+
+__device__ __forceinline__ RowPen row_pen_from(const RowSource &a, int row, int hl_raw, int ne_raw) {
     RowPen r;
     r.nw = 0;
     r.hl = 0;
     r.win_ptr = nullptr;
-    if (a.hist && (a.do_rep || a.do_fp) && a.win > 0) {
-        int hl = a.hist_len[row];
+    if (row_pen_window_on(a)) {
+        int hl = hl_raw;
         hl = hl < 0 ? 0 : (hl > a.hist_ld ? a.hist_ld : hl);
         r.hl = hl;
         r.nw = hl < a.win ? hl : a.win;
@@ -115,7 +121,7 @@ __device__ __forceinline__ RowPen row_pen(const RowSource &a, int row) {
     r.eid = nullptr;
     r.edl = nullptr;
     if (a.edit_ids) {
-        int ne = a.edit_count[row];
+        int ne = ne_raw;
         r.ne = ne < 0 ? 0 : (ne > a.edit_ld ? a.edit_ld : ne);
         r.ne = r.ne > kMaxEdits ? kMaxEdits : r.ne;
         r.eid = a.edit_ids + (int64_t)row * a.edit_ld;
@@ -125,6 +131,10 @@ __device__ __forceinline__ RowPen row_pen(const RowSource &a, int row) {
     r.hs_log2 = n > 0 ? min(11, max(6, 32 - __clz(2 * n - 1))) : 6;
     r.any = n > 0;
     return r;
+}
+
+__device__ __forceinline__ RowPen row_pen(const RowSource &a, int row) {
+    return row_pen_from(a, row, row_pen_window_on(a) ? a.hist_len[row] : 0, a.edit_ids ? a.edit_count[row] : 0);
 }
 
 struct PenRegs {
