@@ -159,9 +159,11 @@ int32_t zi_sample_rows(zi_ctx *ctx, const zi_params *p, const zi_batch *b,
  * the row is never read); group_count [rows] (device) how many, clamped to
  * groups_ld.  Ids g >= ceil(V / 8) are ignored; a group listed twice counts
  * once.  Results are those of zi_sample_rows on the row with the fill
- * written.  Limits: groups_ld <= 1024 (the reference keeps 576), V >= 16,
- * top_k resolving to <= 256 when temp > 0, no final_logit_softcap (it would
- * move the fill to -cap); each returns ZI_ERR_UNSUPPORTED. */
+ * written.  With final_logit_softcap (which runs after the fill and moves it
+ * to -cap*tanh(9)) or top_k resolving to > 256 (lists that order every id),
+ * the filled rows are written to a context scratch, allocated on first use,
+ * and sampled by zi_sample_rows.  Limits: groups_ld <= 1024 (the reference
+ * keeps 576), V >= 16; each returns ZI_ERR_UNSUPPORTED. */
 int32_t zi_sample_rows_pruned(zi_ctx *ctx, const zi_params *p, const zi_batch *b,
                               const uint32_t *groups, const int32_t *group_count,
                               int32_t groups_ld, const float *uniforms,

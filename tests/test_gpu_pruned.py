@@ -181,6 +181,32 @@ def test_pruned_matches_dense_entry(ctx, rows, V, bf16):
         assert np.array_equal(g[key].view(np.uint32), d[key].view(np.uint32)), key
 
 
+@pytest.mark.parametrize("pk,V,bf16", [
+    (dict(temp=0.8, top_k=40, top_p=0.95, min_p=0.05, final_logit_softcap=30.0), 32000, False),
+    (dict(temp=0.8, top_k=40, top_p=0.95, min_p=0.0, final_logit_softcap=2.0), 4096, True),
+    (dict(temp=0.0, repeat_penalty=1.2, penalty_last_n=64, final_logit_softcap=30.0), 32000, False),
+    (dict(temp=0.9, top_k=0, top_p=0.95, min_p=0.05), 32000, False),
+    (dict(temp=0.9, top_k=1000, top_p=0.9, min_p=0.0), 4099, False),
+    (dict(temp=1.0, top_k=0, top_p=1.0, min_p=0.0), 20000, True),
+])
+def test_pruned_dense_path_matches_oracle(ctx, oracle, pk, V, bf16):
+    """Softcap (applied after the fill, so unlisted ids become -cap*tanh(9))
+    and top_k > 256 sample the filled rows through the dense path."""
+    rng = np.random.Generator(np.random.PCG64(V + len(pk)))
+    rows = 4
+    G, cnt = _groups(rng, V, rows, 200)
+    buf, dense = _case_inputs(rng, rows, V, "normal", G, cnt, bf16)
+    u = rng.random((rows, 2), dtype=np.float32)
+    hist = hl = None
+    if "penalty_last_n" in pk:
+        hist = rng.integers(0, V, (rows, 64), dtype=np.uint32)
+        hl = np.full(rows, 64, np.int32)
+    g = _gpu_pruned(ctx, pk, buf, u, G, cnt, hist, hl, bf16=bf16)
+    o = oracle_sample(oracle, pk, dense, u, hist, hl)
+    errs = compare_sample(g, o, pk, V, "pruned dense path")
+    assert not errs, "\n".join(errs[:20])
+
+
 def test_pruned_rejects_unsupported(ctx):
     import torch
     from zinfer_amd._lib import ZI_ERR_INVALID, ZI_ERR_UNSUPPORTED, ZiError
@@ -189,17 +215,12 @@ def test_pruned_rejects_unsupported(ctx):
     V = 4096
     L = torch.zeros((2, V), dtype=torch.float32, device="cuda")
     u = torch.zeros((2, 2), dtype=torch.float32, device="cuda")
-    G = torch.zeros((2, 8), dtype=torch.int32, device="cuda")
     cnt = torch.full((2,), 8, dtype=torch.int32, device="cuda")
-    for pk, code in [(dict(final_logit_softcap=30.0), ZI_ERR_UNSUPPORTED), (dict(top_k=0), ZI_ERR_UNSUPPORTED),
-                     (dict(top_k=1000), ZI_ERR_UNSUPPORTED)]:
-        with pytest.raises(ZiError) as ei:
-            ctx.sample_rows(params(**pk), L, u, vocab=V, groups=G, group_count=cnt)
-        assert ei.value.code == code, pk
     big = torch.zeros((2, 1025), dtype=torch.int32, device="cuda")
     with pytest.raises(ZiError) as ei:
         ctx.sample_rows(params(), L, u, vocab=V, groups=big, group_count=cnt)
     assert ei.value.code == ZI_ERR_UNSUPPORTED
+    G = torch.zeros((2, 8), dtype=torch.int32, device="cuda")
     with pytest.raises(ZiError) as ei:
         ctx.sample_rows(params(), L[:, :15], u, vocab=15, groups=G, group_count=cnt)
     assert ei.value.code in (ZI_ERR_UNSUPPORTED, ZI_ERR_INVALID)

@@ -124,6 +124,7 @@ extern "C" void zi_destroy(zi_ctx *c) {
                     c->g_top2, c->g_tail,  c->win_ids, c->win_len, c->ex_sort, c->nuc_flag};
     for (void *p : ptrs)
         if (p) hipFree(p);
+    if (c->pr_dense) hipFree(c->pr_dense);
     if (c->own_stream) hipStreamDestroy(c->own_stream);
     delete c;
 }
@@ -407,9 +408,32 @@ extern "C" int32_t zi_sample_rows_pruned(zi_ctx *c, const zi_params *p, const zi
     if (groups_ld > zi::kMaxGroupsHost)
         return zi_fail(ZI_ERR_UNSUPPORTED, "%s: groups_ld=%d > %d", fn, groups_ld, zi::kMaxGroupsHost);
     if (b->vocab < 16) return zi_fail(ZI_ERR_UNSUPPORTED, "%s: vocab %d < 16", fn, b->vocab);
-    if (p->final_logit_softcap > 0.0f)  // the cap (model.zig:2492) runs after the fill (:2127) and moves it to -cap
-        return zi_fail(ZI_ERR_UNSUPPORTED, "%s: final_logit_softcap with pruned rows", fn);
     HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+    {
+        const uint32_t V0 = (uint32_t)b->vocab;
+        const uint32_t k0 = (p->top_k == 0 || p->top_k > V0) ? V0 : p->top_k;
+        // The softcap (model.zig:2492) runs after the fill (:2127) and turns it
+        // into -cap*tanh(9); whole-vocabulary and long top-k lists order every
+        // id.  Both take the dense path on the row the reference builds.
+        if (p->final_logit_softcap > 0.0f || (p->temp > 0.0f && k0 > (uint32_t)zi::kMaxTopK)) {
+            const size_t elt = b->dtype == ZI_F32 ? 4 : 2;
+            const size_t need = (size_t)b->rows * (size_t)b->ld * elt;
+            if (need > c->pr_dense_bytes) {
+                if (c->pr_dense) hipFree(c->pr_dense);
+                c->pr_dense = nullptr;
+                c->pr_dense_bytes = 0;
+                hipError_t e = hipMalloc(&c->pr_dense, need);
+                if (e != hipSuccess) return zi_hip_fail(e, "zi_sample_rows_pruned: dense scratch");
+                c->pr_dense_bytes = need;
+            }
+            hipError_t e = zi::launch_pruned_fill(b->logits, c->pr_dense, b->ld, b->vocab, b->rows, b->dtype, groups,
+                                                  group_count, groups_ld, c->stream);
+            if (e != hipSuccess) return zi_hip_fail(e, "pruned fill launch");
+            zi_batch bd = *b;
+            bd.logits = c->pr_dense;
+            return zi_sample_rows(c, p, &bd, uniforms, out);
+        }
+    }
     const zi::Plan pl = zi::plan_rows(b->rows, b->vocab, b->dtype);
     zi::RowSource src;
     rc = fill_source(b, p, true, src, pl, fn);

@@ -27,6 +27,9 @@ struct zi_ctx {
     uint32_t *ex_sort = nullptr;  // 5 x [max_rows][ex_ld] keys in id order, sort keys / ids
     int64_t ex_ld = 0;
     int32_t *nuc_flag = nullptr;  // [max_rows]
+    // pruned rows sampled through the dense path (softcap, top_k > 256), on first use
+    void *pr_dense = nullptr;
+    size_t pr_dense_bytes = 0;
 };
 
 int32_t zi_fail(int32_t code, const char *fmt, ...);

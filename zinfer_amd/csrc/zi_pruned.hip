@@ -402,6 +402,55 @@ __global__ __launch_bounds__(kThreads) void pruned_kernel(SampleParams P) {
     sample_tail<false>(P, row, s.okey, s.oval, k, s.tl, u0, u1);
 }
 
+// One 512-thread workgroup per (row, 4096-id block): the block's listed
+// groups from the row's list (an LDS bitset), then each thread writes one
+// group of 8: copied when listed, -inf otherwise (src/model.zig:2127-2128 then
+// :1156-1158).
+template <typename T>
+__global__ __launch_bounds__(kThreads) void pruned_fill_kernel(const T *src, T *dst, int64_t ld, int V,
+                                                               const uint32_t *groups, const int32_t *group_count,
+                                                               int groups_ld) {
+    constexpr int VEC = VecTraits<T>::VEC;
+    constexpr int NL = 8 / VEC;
+    __shared__ uint32_t bits[kThreads / 32];
+    const int tid = threadIdx.x, row = blockIdx.y;
+    const uint32_t g0 = blockIdx.x * (uint32_t)kThreads;  // first group of this block
+    const uint32_t ngt = ((uint32_t)V + 7) / 8;
+    if (tid < kThreads / 32) bits[tid] = 0u;
+    __syncthreads();
+    int ng = group_count[row];
+    ng = ng < 0 ? 0 : min(ng, min(groups_ld, kMaxGroups));
+    for (int j = tid; j < ng; j += kThreads) {
+        const uint32_t g = groups[(int64_t)row * groups_ld + j];
+        if (g < ngt && g >= g0 && g < g0 + kThreads) atomicOr(&bits[(g - g0) >> 5], 1u << ((g - g0) & 31));
+    }
+    __syncthreads();
+    const uint32_t g = g0 + tid;
+    if (g >= ngt) return;
+    const bool listed = (bits[tid >> 5] >> (tid & 31)) & 1u;
+    const T *s = src + (int64_t)row * ld + g * 8u;
+    T *d = dst + (int64_t)row * ld + g * 8u;
+    const uint32_t ninf = sizeof(T) == 4 ? 0xFF800000u : 0xFF80FF80u;  // -inf, as f32 or two bf16
+#pragma unroll
+    for (int q = 0; q < NL; ++q) {
+        const uint4 v = listed ? *reinterpret_cast<const uint4 *>(s + q * VEC) : make_uint4(ninf, ninf, ninf, ninf);
+        *reinterpret_cast<uint4 *>(d + q * VEC) = v;
+    }
+}
+
+hipError_t launch_pruned_fill(const void *logits, void *dense, int64_t ld, int V, int rows, int dtype,
+                              const uint32_t *groups, const int32_t *group_count, int groups_ld, hipStream_t st) {
+    const int ngt = (V + 7) / 8;
+    dim3 grid((ngt + kThreads - 1) / kThreads, rows), block(kThreads);
+    if (dtype == 0)
+        hipLaunchKernelGGL(pruned_fill_kernel<float>, grid, block, 0, st, static_cast<const float *>(logits),
+                           static_cast<float *>(dense), ld, V, groups, group_count, groups_ld);
+    else
+        hipLaunchKernelGGL(pruned_fill_kernel<uint16_t>, grid, block, 0, st, static_cast<const uint16_t *>(logits),
+                           static_cast<uint16_t *>(dense), ld, V, groups, group_count, groups_ld);
+    return hipGetLastError();
+}
+
 template <typename T, bool M, bool PN>
 static hipError_t launch_pruned_t(const SampleParams &P, int rows, hipStream_t st) {
     hipLaunchKernelGGL((pruned_kernel<T, M, PN>), dim3(rows), dim3(kThreads), 0, st, P);
