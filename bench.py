@@ -616,7 +616,10 @@ def main():
         cpu = {"value": round(n_rows_cpu * creps / tc, 1), "unit": "rows/s", "cores": 1, "kind": "port",
                "sample": f"{n_rows_cpu} rows of the same batch x {creps} passes ({tc:.1f} s), oracle/oracle.c "
                          f"(C restatement of src/sampler.zig:91-276), -O3, 1 thread",
-               "tokens_match_gpu": bool(np.array_equal(gtok, tokc))}
+               "tokens_match_gpu": bool(np.array_equal(gtok, tokc)),
+               # the north star's count of chosen-token disagreements (top-p boundary or other) on the
+               # rows both sides sampled; the kernels are bit-exact, so any nonzero count is a bug
+               "id_mismatches": int(np.count_nonzero(gtok != tokc)), "rows_compared": int(n_rows_cpu)}
 
     out = {
         "metric": METRIC,
