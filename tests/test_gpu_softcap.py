@@ -131,3 +131,43 @@ def test_host_sampler_caps_row_in_place(ctx, oracle):
         assert np.array_equal(got.view(np.uint32), diag["row"].view(np.uint32)), "in-place row differs"
         smp.accept(tok)
         hist.append(tok)
+
+
+def test_softcap_gemma_vocab(ctx, oracle):
+    """Gemma's 262144-entry vocabulary with cap 30 (model.zig's final_logit_softcapping)."""
+    rng = np.random.Generator(np.random.PCG64(262144))
+    rows, V = 8, 262144
+    x, hist, hl, m, ei, ed, ec = _inputs(rng, rows, V, "wide", True, False, False)
+    pk = dict(temp=0.9, top_k=64, top_p=0.95, min_p=0.05, repeat_penalty=1.1, penalty_last_n=128,
+              final_logit_softcap=30.0)
+    u = rng.random((rows, 2), dtype=np.float32)
+    g = gpu_sample(ctx, pk, x, u, hist, hl)
+    o = oracle_sample(oracle, pk, x, u, hist, hl)
+    errs = compare_sample(g, o, pk, V, "gemma")
+    assert not errs, "\n".join(errs[:20])
+
+
+@pytest.mark.parametrize("mode", ["all", "reject"])
+def test_softcap_in_verify(ctx, oracle, mode):
+    """Draft verification with the cap set: every row is capped in the read."""
+    import torch
+
+    from test_gpu_verify import _oracle_loop, _setup
+
+    V, k = 4096, 5
+    pk = dict(temp=0.8, top_k=40, top_p=0.95, min_p=0.05, repeat_penalty=1.2, penalty_last_n=64,
+              final_logit_softcap=6.0, seed=31)
+    smp, rng, hist, stream = _setup(ctx, oracle, V, pk, 55)
+    X = (rng.standard_normal((k + 1, V)) * 6).astype(np.float32)
+    ideal, h, pos = [], list(hist), 0
+    for i in range(k):
+        _, tok, _, pos, h, _ = _oracle_loop(oracle, pk, X[i:i + 1], [], h, stream, pos)
+        ideal.append(tok)
+        h.append(tok)
+    draft = list(ideal)
+    if mode == "reject":
+        draft[1] = (draft[1] + 5) % V
+    exp = _oracle_loop(oracle, pk, X, draft, hist, stream, 0)
+    a, nt, m = smp.verify(torch.from_numpy(X).to("cuda"), draft)
+    assert (a, nt, np.float32(m)) == (exp[0], exp[1], np.float32(exp[2]))
+    assert np.float32(smp.rand_f32()) == np.float32(stream[exp[3]])
