@@ -464,7 +464,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py: this build runs on one GPU only (the sampling path is row-parallel; "
-              "multi-GPU sharding is described in DESIGN.md and not implemented). Use --gpus 1.",
+              "rows would shard across GPUs with no collective, which is not implemented). Use --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
 
