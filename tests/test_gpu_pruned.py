@@ -225,3 +225,22 @@ def test_pruned_rejects_unsupported(ctx):
         ctx.sample_rows(params(), L[:, :15], u, vocab=15, groups=G, group_count=cnt)
     assert ei.value.code in (ZI_ERR_UNSUPPORTED, ZI_ERR_INVALID)
     torch.cuda.synchronize()
+
+
+def test_pruned_counts_clamped_and_empty_rows(ctx, oracle):
+    """group_count above groups_ld is clamped to it; a negative or zero count
+    leaves the whole row at -inf (the reference's fill alone)."""
+    rng = np.random.Generator(np.random.PCG64(31337))
+    rows, V = 4, 32000
+    G, cnt = _groups(rng, V, rows, 100)
+    ld = G.shape[1]
+    cnt = np.array([ld + 50, 0, -3, ld - 20], np.int32)
+    used = np.clip(cnt, 0, ld)
+    x = (rng.standard_normal((rows, V)) * 2).astype(np.float32)
+    dense = np.stack([pruned_row_np(x[r], G[r, :used[r]], V) for r in range(rows)])
+    u = rng.random((rows, 2), dtype=np.float32)
+    for pk in (dict(temp=0.8, top_k=40, top_p=0.95, min_p=0.05), dict(temp=0.0)):
+        g = _gpu_pruned(ctx, pk, x, u, G, cnt)
+        o = oracle_sample(oracle, pk, dense, u)
+        errs = compare_sample(g, o, pk, V, "pruned counts")
+        assert not errs, "\n".join(errs[:20])
