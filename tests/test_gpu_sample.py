@@ -172,3 +172,52 @@ def test_large_batch_rows(ctx, oracle, rows, V, k, kind, pen, mask):
     o = oracle_sample(oracle, pk, x, u, hist, hl, m, ei, ed, ec)
     errs = compare_sample(g, o, pk, V, f"rows{rows}")
     assert not errs, "\n".join(errs[:20])
+
+
+LATE_SCENES = ["leaders", "all_leaders", "neg_edit", "nan_free_mix", "rp_below_one"]
+
+
+@pytest.mark.parametrize("scene", LATE_SCENES)
+def test_late_penalty_select(ctx, oracle, scene):
+    """Penalties that never raise a logit are applied to the chunk's raw
+    candidates only; when penalized leaders drop below the candidate
+    threshold (or an edit delta is negative) the kernel penalizes its
+    registers and selects again.  Both branches must match the oracle."""
+    rng = np.random.Generator(np.random.PCG64(4200 + LATE_SCENES.index(scene)))
+    rows, V = 8, 128256
+    x = (rng.standard_t(3, (rows, V)) * 2).astype(np.float32)
+    u = rng.random((rows, 2), dtype=np.float32)
+    order = np.argsort(-x, axis=1, kind="stable")
+    H = 256
+    hist = rng.integers(0, V, (rows, H), dtype=np.uint32)
+    pk = dict(temp=0.7, top_k=50, top_p=0.9, min_p=0.05, repeat_penalty=1.15, freq_penalty=0.3,
+              presence_penalty=0.5, penalty_last_n=256)
+    ei = ed = ec = None
+    if scene == "leaders":  # a few leaders penalized: candidates stay >= k
+        hist[:, -3:] = order[:, :3]
+    elif scene == "all_leaders":  # every leader penalized hard: the fallback selects again
+        hist[:, :200] = order[:, :200]
+        pk.update(repeat_penalty=3.0, presence_penalty=4.0)
+    elif scene == "neg_edit":  # an edit that raises a logit: fallback in that chunk
+        E = 8
+        ei = np.stack([rng.choice(V, size=E, replace=False) for _ in range(rows)]).astype(np.uint32)
+        ed = (rng.random((rows, E)) * 2).astype(np.float32)
+        ed[::2, 0] = -25.0  # lifts a random id into the top-k
+        ec = np.full(rows, E, np.int32)
+    elif scene == "nan_free_mix":  # penalized leaders with zero edits and short windows
+        hist[:, -40:] = order[:, 10:50]
+        E = 4
+        ei = np.ascontiguousarray(order[:, :E]).astype(np.uint32)
+        ed = np.zeros((rows, E), np.float32)
+        ed[:, 1] = 0.75
+        ec = np.arange(rows, dtype=np.int32) % (E + 1)
+    elif scene == "rp_below_one":  # raises negative logits: the in-stream penalty path
+        hist[:, -20:] = order[:, :20]
+        pk.update(repeat_penalty=0.9)
+    hist_len = np.full(rows, H, np.int32)
+    hist_len[1] = 0
+    hist_len[2] = 17
+    g = gpu_sample(ctx, pk, x, u, hist, hist_len, None, ei, ed, ec)
+    o = oracle_sample(oracle, pk, x, u, hist, hist_len, None, ei, ed, ec)
+    errs = compare_sample(g, o, pk, V, f"late-{scene}")
+    assert not errs, "\n".join(errs[:20])

@@ -589,6 +589,7 @@ struct SelectLds {
     float sval[kCapA];
     uint32_t rank[kSortMax];
     int wcnt[kWaves];
+    int wge[kWaves];  // late penalties: candidates still >= tau, per wave
 };
 
 // This wave's candidates: the elements >= tau of its staged vector pairs and
@@ -874,6 +875,137 @@ __device__ __forceinline__ void chunk_select_publish(const RowSource &a, ChunkRe
     }
     __syncthreads();
     rank_publish(sl.skey, sl.sval, min(*s_n, kCapA), k, sl.rank, out);
+}
+
+// ------------------------------------------- stage A with late penalties
+// For penalties that never raise a logit (repetition penalty >= 1, frequency
+// and presence >= 0, edit deltas >= 0) the chunk is selected on its raw
+// values and only the candidates are penalized, so nothing in the stream
+// waits for the history, which arrives behind the row.
+//
+// Why it is exact: C = every raw value >= tau.  A value outside C is below
+// tau before its penalty and so after it.  Penalize C in place; if at least k
+// of C are still >= tau, the chunk's top-k lie in C and rank_regions ranks
+// them by their penalized keys.  Otherwise (penalized candidates fell below
+// tau) the penalties are applied to the registers and the plain select runs.
+
+// Clears the id -> (count, delta) hash (the bitset is not used here).
+__device__ __forceinline__ void pen_clear_hash(PenTable &t) {
+    for (int i = threadIdx.x; i < kHashMax; i += kThreads) {
+        t.key[i] = 0u;
+        t.cnt[i] = 0u;
+        t.delta[i] = 0.0f;
+    }
+}
+
+// Fills the hash with the chunk's window ids (counts) and edits (deltas).
+// Returns true when an edit of this chunk has a delta that is negative or
+// NaN, which could raise a logit.  No barrier.
+__device__ __forceinline__ bool pen_count_late(PenTable &t, const RowPen &rp, const PenRegs &pr, int c0, int c1) {
+#pragma unroll
+    for (int u = 0; u < kWinPerThread; ++u) {
+        const uint32_t id = pr.w[u];
+        if (id >= (uint32_t)c0 && id < (uint32_t)c1) atomicAdd(&t.cnt[pen_insert(t, id, rp.hs_log2)], 1u);
+    }
+    bool bad = false;
+    if (pr.e >= (uint32_t)c0 && pr.e < (uint32_t)c1) {
+        t.delta[pen_insert(t, pr.e, rp.hs_log2)] = pr.d;
+        bad = !(pr.d >= 0.0f);
+    }
+    return bad;
+}
+
+// Slot of `id` in the hash, or -1.  The table holds at least twice as many
+// slots as ids, so an empty slot ends every probe.
+__device__ __forceinline__ int pen_find(const PenTable &t, uint32_t id, int hs_log2) {
+    uint32_t h = hash_slot(id, hs_log2);
+    const uint32_t m = (1u << hs_log2) - 1;
+    for (;;) {
+        const uint32_t kk = t.key[h];
+        if (kk == id + 1) return (int)h;
+        if (kk == 0u) return -1;
+        h = (h + 1) & m;
+    }
+}
+
+// The chunk's selection after chunk_stream without penalties: `tau` from
+// select_prepare (raw lane maxima), `pr` from pen_prefetch, hl_raw / ne_raw
+// the row's hist_len / edit_count as loaded, `t` cleared by pen_clear_hash
+// before a barrier that precedes this call, *s_bad zero.  Publishes the
+// chunk's exact penalized top-k like chunk_select_publish.
+template <typename T, int NV>
+__device__ __forceinline__ void chunk_select_late(const RowSource &a, int row, ChunkRegs<T, NV> &cr, int c0, int c1,
+                                                  int k, SelectLds<T, NV> &sl, PenTable &t, PenRegs &pr, int hl_raw,
+                                                  int ne_raw, uint32_t *s_tau, int *s_n, int *s_bad, uint32_t *bins,
+                                                  int *s_dig, ChunkOut out, float tau) {
+    constexpr int VEC = VecTraits<T>::VEC;
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int wc = wave_candidates<T, NV, false>(a, cr, c0, tau, sl, nullptr, nullptr);
+    const RowPen rp = row_pen_from(a, row, row_pen_window_on(a) ? hl_raw : 0, a.edit_ids ? ne_raw : 0);
+    pen_window(rp, pr);
+    if (pen_count_late(t, rp, pr, c0, c1)) *s_bad = 1;
+    if (lane == 0) sl.wcnt[wid] = wc;
+    __syncthreads();  // hash, wave counts and the bad-edit flag complete
+    int off[kWaves + 1];
+    off[0] = 0;
+    bool overflow = *s_bad != 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+        overflow |= sl.wcnt[w] > kWaveCand;
+        off[w + 1] = off[w] + min(sl.wcnt[w], kWaveCand);
+    }
+    if (!overflow && off[kWaves] <= kSortMax) {  // uniform
+        const int nw = off[wid + 1] - off[wid];   // <= kWaveCand = 64: one entry per lane
+        bool ge = false;
+        if (lane < nw) {
+            float x = sl.wval[wid][lane];
+            if (rp.any) {
+                const uint32_t id = ckey_id(sl.wkey[wid][lane]);
+                const int h = pen_find(t, id, rp.hs_log2);
+                if (h >= 0) {
+                    x = pen_apply(x, t.cnt[h], t.delta[h], a);
+                    sl.wkey[wid][lane] = ckey(x, id);
+                    sl.wval[wid][lane] = x;
+                }
+            }
+            ge = x >= tau;
+        }
+        const uint64_t b = ballot(ge);
+        if (lane == 0) sl.wge[wid] = __popcll(b);
+        __syncthreads();  // penalized regions and counts complete
+        int nge = 0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) nge += sl.wge[w];
+        if (nge >= k) {  // uniform
+            rank_regions<T, NV>(sl, off, k, out);
+            return;
+        }
+    }
+    // Fallback: penalize the registers (every element probes the hash) and
+    // select from scratch.  select_prepare's barriers order its LDS writes
+    // after every read above.
+    if (rp.any) {
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int e0 = c0 + (j * kThreads + tid) * VEC;
+            float m = __builtin_nanf("");
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) {
+                float x = cr.x[j * VEC + e];
+                if (x == x) {
+                    const int h = pen_find(t, (uint32_t)(e0 + e), rp.hs_log2);
+                    if (h >= 0) x = pen_apply(x, t.cnt[h], t.delta[h], a);
+                    cr.x[j * VEC + e] = x;
+                }
+                m = fmaxf(m, x);
+            }
+            cr.m4[j] = m;
+            tmax = fmaxf(tmax, m);
+        }
+        cr.lmax = tmax;
+    }
+    chunk_select_publish<T, NV, false>(a, cr, c0, k, sl, nullptr, nullptr, s_tau, s_n, bins, s_dig, out);
 }
 
 // ------------------------------------------------------------- stage B

@@ -43,7 +43,28 @@ struct SampleStageB {
     TailLds tl;
 };
 
-template <typename T, int NV, bool HAS_MASK, bool HAS_PEN, bool CAP>
+// Stage B, run by the last workgroup of the row: merges the G sorted chunk
+// lists and runs the reference tail on wave 0.
+__device__ __forceinline__ void sample_stage_b(const SampleParams &P, int row, int G, int k, SampleStageB &b,
+                                               float u0, float u1) {
+    const int n = row_merge(P.g_key, P.g_val, P.g_cnt, row, G, k, b.ml, b.okey, b.oval);
+    if (threadIdx.x >= 64) return;  // the tail runs on wave 0 with all 64 lanes active
+    if (n == 0) {                   // no selectable logit (every entry NaN): outside the reference contract
+        if (threadIdx.x == 0) {
+            P.tok[row] = 0u;
+            P.margin[row] = 10.0f;
+            if (P.ndraws) P.ndraws[row] = 0;
+            if (P.keep) P.keep[row] = 0;
+        }
+        return;
+    }
+    sample_tail<false>(P, row, b.okey, b.oval, n, b.tl, u0, u1);
+}
+
+// LATE (with HAS_PEN, for penalties that never raise a logit): the stream
+// runs without the penalty inputs and only the chunk's candidates are
+// penalized (chunk_select_late).
+template <typename T, int NV, bool HAS_MASK, bool HAS_PEN, bool CAP, bool LATE>
 __global__ __launch_bounds__(kThreads) void sample_kernel(SampleParams P) {
     __shared__ union {
         SampleStageA<T, NV, HAS_PEN> a;
@@ -52,7 +73,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleParams P) {
     __shared__ uint32_t s_bins[256];
     __shared__ uint32_t s_tau[1];
     __shared__ int s_dig[2];
-    __shared__ int s_n, s_flag;
+    __shared__ int s_n, s_flag, s_bad;
 
     const RowSource &a = P.src;
     const int tid = threadIdx.x;
@@ -65,12 +86,40 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleParams P) {
 
     PenTable *pen = nullptr;
     if constexpr (HAS_PEN) pen = &sm.a.p.pen;
-    PenOwn own;
     ChunkRegs<T, NV> cr;
     // The candidate threshold is computed from the first kSplit vectors while
     // the last ones are still arriving.
     constexpr int kSplit = NV * 3 / 4;
     float tau = 0.0f;
+    const int64_t rg = (int64_t)row * G + g;
+    ChunkOut out{P.g_key + rg * kCapA, P.g_val + rg * kCapA, P.g_cnt + rg};
+    if constexpr (LATE) {
+        static_assert(HAS_PEN, "late penalties need the penalty table");
+        // Penalty inputs first, as vector loads (lane-varying addresses), so
+        // that waiting for them after the stream waits for nothing else.
+        PenRegs pr;
+        pen_prefetch(a, row, pr);
+        int rv = row;
+        asm volatile("" : "+v"(rv));
+        const int hl_raw = row_pen_window_on(a) ? a.hist_len[rv] : 0;
+        const int ne_raw = a.edit_ids ? a.edit_count[rv] : 0;
+        if (tid == 0) s_bad = 0;
+        auto mid = [&](float lmax) {
+            pen_clear_hash(*pen);  // ordered before the inserts by the barriers below
+            tau = select_prepare<T, NV>(lmax, k, sm.a.sel, s_tau, &s_n);
+        };
+        chunk_stream<T, NV, HAS_MASK, false, CAP, NoHook, kSplit>(a, row, c0, c1, cr, nullptr, nullptr, NoHook(),
+                                                                   mid);
+        int ur = 2 * row;
+        asm volatile("" : "+v"(ur));
+        const float u0 = P.uniforms[ur], u1 = P.uniforms[ur + 1];
+        chunk_select_late<T, NV>(a, row, cr, c0, c1, k, sm.a.sel, *pen, pr, hl_raw, ne_raw, s_tau, &s_n, &s_bad,
+                                 s_bins, s_dig, out, tau);
+        if (!row_ticket(P.tickets, row, G, &s_flag)) return;
+        sample_stage_b(P, row, G, k, sm.b, u0, u1);
+        return;
+    }
+    PenOwn own;
     auto mid = [&](float lmax) { tau = select_prepare<T, NV>(lmax, k, sm.a.sel, s_tau, &s_n); };
     chunk_stream<T, NV, HAS_MASK, HAS_PEN, CAP, NoHook, kSplit>(a, row, c0, c1, cr, pen, &own, NoHook(), mid);
     // This row's two uniforms, requested now so that the tail never waits
@@ -79,25 +128,10 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleParams P) {
     int ur = 2 * row;
     asm volatile("" : "+v"(ur));
     const float u0 = P.uniforms[ur], u1 = P.uniforms[ur + 1];
-    const int64_t rg = (int64_t)row * G + g;
-    ChunkOut out{P.g_key + rg * kCapA, P.g_val + rg * kCapA, P.g_cnt + rg};
     chunk_select_publish<T, NV, HAS_PEN, true>(a, cr, c0, k, sm.a.sel, pen, &own, s_tau, &s_n, s_bins, s_dig, out,
                                                tau);
     if (!row_ticket(P.tickets, row, G, &s_flag)) return;
-
-    // ---------------- stage B: the last workgroup of this row ----------------
-    const int n = row_merge(P.g_key, P.g_val, P.g_cnt, row, G, k, sm.b.ml, sm.b.okey, sm.b.oval);
-    if (tid >= 64) return;  // the tail runs on wave 0 with all 64 lanes active
-    if (n == 0) {           // no selectable logit (every entry NaN): outside the reference contract
-        if (tid == 0) {
-            P.tok[row] = 0u;
-            P.margin[row] = 10.0f;
-            if (P.ndraws) P.ndraws[row] = 0;
-            if (P.keep) P.keep[row] = 0;
-        }
-        return;
-    }
-    sample_tail<false>(P, row, sm.b.okey, sm.b.oval, n, sm.b.tl, u0, u1);
+    sample_stage_b(P, row, G, k, sm.b, u0, u1);
 }
 
 // Per-thread running (ref, S) with S = sum exp(x - ref) over the thread's
@@ -430,8 +464,18 @@ static hipError_t launch_sample_t(const SampleParams &P, int rows, hipStream_t s
         return hipGetLastError();
     }
     dim3 grid(rows * P.src.G), block(kThreads);
-    if constexpr (NUC) hipLaunchKernelGGL((nucleus_kernel<T, NV, M, PN, CAP>), grid, block, 0, st, P);
-    else hipLaunchKernelGGL((sample_kernel<T, NV, M, PN, CAP>), grid, block, 0, st, P);
+    if constexpr (NUC) {
+        hipLaunchKernelGGL((nucleus_kernel<T, NV, M, PN, CAP>), grid, block, 0, st, P);
+    } else if constexpr (PN) {
+        // Penalties that never raise a logit (edits are checked per chunk in
+        // the kernel) take the late-penalty select.
+        const RowSource &a = P.src;
+        const bool late = (!a.do_rep || a.rp >= 1.0f) && (!a.do_fp || (a.freq >= 0.0f && a.pres >= 0.0f));
+        if (late) hipLaunchKernelGGL((sample_kernel<T, NV, M, PN, CAP, true>), grid, block, 0, st, P);
+        else hipLaunchKernelGGL((sample_kernel<T, NV, M, PN, CAP, false>), grid, block, 0, st, P);
+    } else {
+        hipLaunchKernelGGL((sample_kernel<T, NV, M, PN, CAP, false>), grid, block, 0, st, P);
+    }
     return hipGetLastError();
 }
 
