@@ -310,25 +310,45 @@ struct NoMid {
 // (the penalty hash is filled just before it) while the remaining vectors'
 // loads are still in flight; workgroup barriers inside mid order LDS only and
 // do not wait for them.
+// PF: the chunk's logit vectors were requested by the caller into pf[]
+// (chunk_request); as each one is unpacked, its register is refilled with the
+// same vector of the next chunk [n0, n1) (none when n0 >= n1), so that chunk's
+// loads are in flight while the caller selects from this one.
+template <typename T, int NV>
+__device__ __forceinline__ void chunk_request(const RowSource &a, int row, int c0, int c1, uint4 (&pf)[NV]) {
+    constexpr int VEC = VecTraits<T>::VEC;
+    const int nvec = (c1 - c0 + VEC - 1) / VEC;
+    const T *base = reinterpret_cast<const T *>(a.logits) + (int64_t)row * a.ld + c0;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int q = min(j * kThreads + (int)threadIdx.x, nvec - 1);
+        pf[j] = ld_stream(reinterpret_cast<const uint4 *>(base + q * VEC));
+    }
+}
+
 template <typename T, int NV, bool HAS_MASK, bool HAS_PEN, bool CAP = false, class Hook = NoHook, int SPLIT = NV,
-          class Mid = NoMid>
+          class Mid = NoMid, bool PF = false>
 __device__ __forceinline__ float chunk_stream(const RowSource &a, int row, int c0, int c1, ChunkRegs<T, NV> &cr,
-                                              PenTable *t, PenOwn *own, Hook hook = Hook(), Mid mid = Mid()) {
+                                              PenTable *t, PenOwn *own, Hook hook = Hook(), Mid mid = Mid(),
+                                              uint4 *pf = nullptr, int n0 = 0, int n1 = 0) {
     constexpr int VEC = VecTraits<T>::VEC;
     const int tid = threadIdx.x;
     const int nvec = (c1 - c0 + VEC - 1) / VEC;
     const T *base = reinterpret_cast<const T *>(a.logits) + (int64_t)row * a.ld + c0;
     const uint32_t *mrow = HAS_MASK ? a.mask + (int64_t)row * a.mask_ld : nullptr;
+    const int nvec_next = (n1 - n0 + VEC - 1) / VEC;
+    const T *base_next = reinterpret_cast<const T *>(a.logits) + (int64_t)row * a.ld + n0;
 
     PenRegs pr;
     if (HAS_PEN) pen_prefetch(a, row, pr);
     // the row's loads depend on nothing that waits for memory
-    uint4 raw[NV];
+    uint4 raw_own[NV];
+    uint4 *raw = PF ? pf : raw_own;
     uint32_t mw[NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         int q = min(j * kThreads + tid, nvec - 1);
-        raw[j] = ld_stream(reinterpret_cast<const uint4 *>(base + q * VEC));
+        if (!PF) raw[j] = ld_stream(reinterpret_cast<const uint4 *>(base + q * VEC));
         if (HAS_MASK) mw[j] = mrow[(c0 + q * VEC) >> 5];
     }
     uint32_t pw[NV];
@@ -350,6 +370,12 @@ __device__ __forceinline__ float chunk_stream(const RowSource &a, int row, int c
         const int id0 = c0 + q * VEC;
         float v[VEC];
         unpack<T>(raw[j], v);
+        if constexpr (PF) {
+            if (n0 < n1) {  // uniform
+                const int nq = min(j * kThreads + tid, nvec_next - 1);
+                raw[j] = ld_stream(reinterpret_cast<const uint4 *>(base_next + nq * VEC));
+            }
+        }
         if constexpr (CAP) {
 #pragma unroll
             for (int e = 0; e < VEC; ++e) v[e] = softcap_f(v[e], a.cap, a.inv_cap);

@@ -308,11 +308,18 @@ __global__ __launch_bounds__(kThreads) void row_kernel(SampleParams P) {
     // The row in steps of what the registers hold (the plan's chunking only
     // sets the layout of the row-total record below).
     constexpr int SUB = kThreads * NV * VecTraits<T>::VEC;
+    // bf16 rows of up to 32 elements per thread per step: each step's loads
+    // are requested during the previous step (NV registers stay live through
+    // the select; larger steps would spill).
+    constexpr bool PF = std::is_same<T, uint16_t>::value && NV <= 4;
+    uint4 pf[NV];
+    if constexpr (PF) chunk_request<T, NV>(a, row, 0, min(a.V, SUB), pf);
     for (int c0 = 0; c0 < a.V; c0 += SUB) {
         const int c1 = min(a.V, c0 + SUB);
         PenOwn own;
         ChunkRegs<T, NV> cr;
-        chunk_stream<T, NV, HAS_MASK, HAS_PEN, CAP>(a, row, c0, c1, cr, pen, &own);
+        chunk_stream<T, NV, HAS_MASK, HAS_PEN, CAP, NoHook, NV, NoMid, PF>(a, row, c0, c1, cr, pen, &own, NoHook(),
+                                                                          NoMid(), pf, c1, min(a.V, c1 + SUB));
         float tau;
         if constexpr (by_max) {
             const float lm = cr.lmax;
