@@ -184,7 +184,7 @@ def test_late_penalty_select(ctx, oracle, scene):
     threshold (or an edit delta is negative) the kernel penalizes its
     registers and selects again.  Both branches must match the oracle."""
     rng = np.random.Generator(np.random.PCG64(4200 + LATE_SCENES.index(scene)))
-    rows, V = 8, 128256
+    rows, V = 16, 128256  # 64 workgroups: the late-penalty select is taken from that grid size
     x = (rng.standard_t(3, (rows, V)) * 2).astype(np.float32)
     u = rng.random((rows, 2), dtype=np.float32)
     order = np.argsort(-x, axis=1, kind="stable")

@@ -23,6 +23,7 @@
 namespace zi {
 
 constexpr int kRowLoopRows = 256;  // batches this large run one workgroup per row
+constexpr int kLatePenMinGroups = 64;  // grids from a quarter of the CUs take the late-penalty select
 
 template <bool P>
 struct PenLds {
@@ -475,9 +476,13 @@ static hipError_t launch_sample_t(const SampleParams &P, int rows, hipStream_t s
         hipLaunchKernelGGL((nucleus_kernel<T, NV, M, PN, CAP>), grid, block, 0, st, P);
     } else if constexpr (PN) {
         // Penalties that never raise a logit (edits are checked per chunk in
-        // the kernel) take the late-penalty select.
+        // the kernel) take the late-penalty select when the grid is large
+        // enough for the history to arrive behind other workgroups' rows
+        // (config 1, 4 workgroups, measured 0.13 us faster with the
+        // in-stream penalties; config 2, 256 workgroups, 0.72 us slower).
         const RowSource &a = P.src;
-        const bool late = (!a.do_rep || a.rp >= 1.0f) && (!a.do_fp || (a.freq >= 0.0f && a.pres >= 0.0f));
+        const bool late = rows * a.G >= kLatePenMinGroups && (!a.do_rep || a.rp >= 1.0f) &&
+                          (!a.do_fp || (a.freq >= 0.0f && a.pres >= 0.0f));
         if (late) hipLaunchKernelGGL((sample_kernel<T, NV, M, PN, CAP, true>), grid, block, 0, st, P);
         else hipLaunchKernelGGL((sample_kernel<T, NV, M, PN, CAP, false>), grid, block, 0, st, P);
     } else {
