@@ -108,3 +108,43 @@ def test_apply_mask_rows(ctx, oracle, bf16):
         exp = oracle.apply_mask(x[r], mask[r])
         assert np.array_equal(f32bits(got[r]), f32bits(exp))
     assert np.all(L[:, V:].float().cpu().numpy() == 0)  # padding untouched
+
+
+WALK_CASES = [  # (rows, V, k, bf16): rows x chunks > 256 takes the walking entropy kernel
+    (40, 262144, 8, False),    # 6 segments per row, ragged last segment and step
+    (60, 131073, 1, False),    # 4 segments, V not a multiple of the step
+    (300, 20000, 64, False),   # one workgroup walks each whole row (2 steps)
+    (64, 151936, 8, True),     # bf16 steps of 32 elements per thread
+]
+
+
+@pytest.mark.parametrize("rows,V,k,bf16", WALK_CASES)
+def test_entropy_walk_rows(ctx, oracle, rows, V, k, bf16):
+    """Segments walked by one workgroup each: a running top-k in LDS whose
+    k-th value is each later step's threshold.  Rows with ties, -inf runs, a
+    dominant logit and increasing values (every step beats the running
+    list) cover the threshold's overflow paths."""
+    from zinfer_amd.workloads import _bf16_round
+
+    rng = np.random.Generator(np.random.PCG64(rows * 7 + k))
+    x = (rng.standard_normal((rows, V)) * 2).astype(np.float32)
+    x[1, V - 3] += 15  # dominant logit in the last step
+    x[2, rng.random(V) < 0.7] = -np.inf
+    x[3, :] = np.round(x[3, :])  # ties across steps and segments
+    x[4, :] = np.linspace(-5.0, 5.0, V, dtype=np.float32)  # increasing: each step overflows the running list
+    x[5, :] = -np.inf
+    x[5, 12345 % V] = 0.0
+    if bf16:
+        x = _bf16_round(x)
+    draft = rng.integers(0, V, rows).astype(np.uint32)
+    draft[1] = V - 3
+    ent, ids, probs, am, acc = ctx.entropy_topk_rows(to_device(x, bf16=bf16), k, dev(draft.astype(np.int32)),
+                                                     vocab=V)
+    ent, ids, probs, am, acc = (t.cpu().numpy() for t in (ent, ids, probs, am, acc))
+    for r in range(rows):
+        H, eids, eprobs = oracle.entropy_topk(x[r], k)
+        n = len(eids)
+        assert abs(ent[r] - H) <= 1e-5 * abs(H) + 1e-7, (r, ent[r], H)
+        assert np.array_equal(ids[r][:n].astype(np.uint32), eids), (r, ids[r][:n], eids)
+        np.testing.assert_allclose(probs[r][:n], eprobs, rtol=1e-5, atol=1e-30)
+        assert am[r] == eids[0] and acc[r] == int(eids[0] == draft[r])

@@ -2,6 +2,7 @@
 // planning and kernel dispatch for the batched device entry points.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -496,6 +497,8 @@ extern "C" int32_t zi_argmax_rows(zi_ctx *c, const zi_batch *b, uint32_t *out_to
     return run_argmax(c, src, b, pl, out_tok, out_margin, out_tok_low, out_margin_true, nullptr);
 }
 
+static constexpr int kWalkGroups = 256;  // one workgroup per CU
+
 extern "C" int32_t zi_entropy_topk_rows(zi_ctx *c, const zi_batch *b, int32_t k, const uint32_t *draft,
                                         float *out_entropy, uint32_t *out_ids, float *out_probs, int32_t out_ld,
                                         uint32_t *out_argmax, uint8_t *out_accept) {
@@ -507,7 +510,17 @@ extern "C" int32_t zi_entropy_topk_rows(zi_ctx *c, const zi_batch *b, int32_t k,
         return zi_fail(ZI_ERR_INVALID, "zi_entropy_topk_rows: out_ld=%d < k=%d", out_ld, k);
     if (out_accept && !draft) return zi_fail(ZI_ERR_INVALID, "zi_entropy_topk_rows: out_accept needs draft");
     HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
-    const zi::Plan pl = zi::plan_rows(b->rows, b->vocab, b->dtype);
+    zi::Plan pl = zi::plan_rows(b->rows, b->vocab, b->dtype);
+    // A chunked grid of more than one workgroup per CU would run in rounds
+    // that do not overlap; walking workgroups (one round) take such batches.
+    const bool walk = (int64_t)b->rows * pl.G > kWalkGroups;
+    if (walk) {
+        const int gw = std::max(1, std::min(zi::kMaxGHost, kWalkGroups / b->rows));
+        int ch = (b->vocab + gw - 1) / gw;
+        ch = (ch + 63) / 64 * 64;
+        pl.G = (b->vocab + ch - 1) / ch;
+        pl.CH = ch;
+    }
     zi::EntropyParams P;
     std::memset(&P, 0, sizeof P);
     rc = fill_source(b, nullptr, false, P.src, pl, "zi_entropy_topk_rows");
@@ -525,7 +538,8 @@ extern "C" int32_t zi_entropy_topk_rows(zi_ctx *c, const zi_batch *b, int32_t k,
     P.g_cnt = c->g_cnt;
     P.g_stat = c->g_stat;
     P.tickets = c->tickets;
-    hipError_t e = zi::launch_entropy(P, b->dtype, pl.nv, b->rows, c->stream);
+    hipError_t e = walk ? zi::launch_entropy_walk(P, b->dtype, b->rows, c->stream)
+                        : zi::launch_entropy(P, b->dtype, pl.nv, b->rows, c->stream);
     if (e != hipSuccess) return zi_hip_fail(e, "entropy kernel launch");
     return ZI_OK;
 }

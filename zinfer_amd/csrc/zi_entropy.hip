@@ -8,9 +8,10 @@
 //   M = max x, Z = sum exp(x - M), A = sum exp(x - M) (x - M),
 //   H = ln Z - A / Z,  p_i = exp(x_i - M) / Z.
 // Each thread keeps (ref, S, U) with S = sum exp(x - ref), U = sum exp(x -
-// ref)(x - ref) over its elements; ref moves up only when an element exceeds
-// it by 64 so the f32 sums cannot overflow.  Workgroup and row merges are in
-// f64.
+// ref)(x - ref) over its elements; ref is the thread's running maximum, so
+// every term is at most 1 and no small term is added to a sum dominated by a
+// far larger one (a dominant logit after small ones would otherwise round the
+// later terms away).  Workgroup and row merges are in f64.
 #include "zi_launch.hpp"
 #include "zi_rowpass.hpp"
 
@@ -31,7 +32,7 @@ struct EntHook {
     float *ref, *S, *U;
     template <int VEC>
     __device__ void operator()(int, const float (&v)[VEC], float m4) const {
-        if (m4 > *ref + 64.0f) {  // also the first finite value (ref = -inf)
+        if (m4 > *ref) {  // also the first finite value (ref = -inf)
             if (*ref != -INFINITY) {
                 float dl = *ref - m4;
                 float sc = __builtin_amdgcn_exp2f(dl * kLog2e);
@@ -50,6 +51,57 @@ struct EntHook {
     }
 };
 
+struct EntLds {
+    float wmax[kWaves];
+    double ws[kWaves], wu[kWaves];
+    double M, Z;
+};
+
+// Workgroup merge of every thread's (ref, S, U) in f64 into sl.wmax / ws / wu
+// (per wave); contains a barrier, and the per-wave sums are read after the
+// caller's next barrier.
+__device__ __forceinline__ void ent_stats_reduce(float ref, float S, float U, EntLds &sl) {
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    float wm = wave_max_f(ref);
+    if (lane == 0) sl.wmax[wid] = wm;
+    __syncthreads();
+    float M = sl.wmax[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) M = fmaxf(M, sl.wmax[w]);
+    double ds = 0.0, du = 0.0;
+    if (ref != -INFINITY && M != -INFINITY) {
+        double sh = (double)ref - (double)M;
+        double sc = exp(sh);
+        ds = (double)S * sc;
+        du = ((double)U + sh * (double)S) * sc;
+    }
+    ds = wave_sum_d(ds);
+    du = wave_sum_d(du);
+    if (lane == 0) {
+        sl.ws[wid] = ds;
+        sl.wu[wid] = du;
+    }
+}
+
+// Thread 0 stores the workgroup's (max, S, U) record for chunk rg (after a
+// barrier that follows ent_stats_reduce).
+__device__ __forceinline__ void ent_stats_publish(const EntropyParams &P, int64_t rg, const EntLds &sl) {
+    if (threadIdx.x != 0) return;
+    float M = sl.wmax[0];
+    double ts = 0.0, tu = 0.0;
+    for (int w = 0; w < kWaves; ++w) {
+        M = fmaxf(M, sl.wmax[w]);
+        ts += sl.ws[w];
+        tu += sl.wu[w];
+    }
+    st_agent(&P.g_stat[rg * 3], (double)M);
+    st_agent(&P.g_stat[rg * 3 + 1], ts);
+    st_agent(&P.g_stat[rg * 3 + 2], tu);
+}
+
+__device__ __forceinline__ void entropy_stage_b(const EntropyParams &P, int row, int G, int k, EntStageB &b,
+                                                EntLds &sl);
+
 template <typename T, int NV>
 __global__ __launch_bounds__(kThreads) void entropy_kernel(EntropyParams P) {
     __shared__ union {
@@ -60,12 +112,9 @@ __global__ __launch_bounds__(kThreads) void entropy_kernel(EntropyParams P) {
     __shared__ uint32_t s_tau[1];
     __shared__ int s_dig[2];
     __shared__ int s_n, s_flag;
-    __shared__ float s_wmax[kWaves];
-    __shared__ double s_ws[kWaves], s_wu[kWaves];
-    __shared__ double s_M, s_Z;
+    __shared__ EntLds sl;
 
     const RowSource &a = P.src;
-    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int G = a.G;
     const int row = blockIdx.x / G;
     const int g = blockIdx.x - row * G;
@@ -78,44 +127,23 @@ __global__ __launch_bounds__(kThreads) void entropy_kernel(EntropyParams P) {
     chunk_stream<T, NV, false, false, false, EntHook>(a, row, c0, c1, cr, nullptr, nullptr,
                                                       EntHook{&ref, &S, &U});
 
-    // workgroup merge of (ref, S, U) in f64
-    float wm = wave_max_f(ref);
-    if (lane == 0) s_wmax[wid] = wm;
-    __syncthreads();
-    float M = s_wmax[0];
-#pragma unroll
-    for (int w = 1; w < kWaves; ++w) M = fmaxf(M, s_wmax[w]);
-    double ds = 0.0, du = 0.0;
-    if (ref != -INFINITY && M != -INFINITY) {
-        double sh = (double)ref - (double)M;
-        double sc = exp(sh);
-        ds = (double)S * sc;
-        du = ((double)U + sh * (double)S) * sc;
-    }
-    ds = wave_sum_d(ds);
-    du = wave_sum_d(du);
-    if (lane == 0) {
-        s_ws[wid] = ds;
-        s_wu[wid] = du;
-    }
-
     const int64_t rg = (int64_t)row * G + g;
+    ent_stats_reduce(ref, S, U, sl);
     ChunkOut out{P.g_key + rg * kCapA, P.g_val + rg * kCapA, P.g_cnt + rg};
     chunk_select_publish<T, NV, false>(a, cr, c0, k, sm.a.sel, nullptr, nullptr, s_tau, &s_n, s_bins, s_dig, out);
-    if (tid == 0) {
-        double ts = 0.0, tu = 0.0;
-        for (int w = 0; w < kWaves; ++w) {
-            ts += s_ws[w];
-            tu += s_wu[w];
-        }
-        st_agent(&P.g_stat[rg * 3], (double)M);
-        st_agent(&P.g_stat[rg * 3 + 1], ts);
-        st_agent(&P.g_stat[rg * 3 + 2], tu);
-    }
+    ent_stats_publish(P, rg, sl);
     if (!row_ticket(P.tickets, row, G, &s_flag)) return;
+    entropy_stage_b(P, row, G, k, sm.b, sl);
+}
 
-    // ---------------- last workgroup of the row ----------------
-    const int n = row_merge(P.g_key, P.g_val, P.g_cnt, row, G, k, sm.b.ml, sm.b.okey, sm.b.oval);
+// The last workgroup of the row: merges the G sorted lists, the G (max, S, U)
+// records into the entropy, and writes the top-k with full-vocabulary
+// probabilities, the argmax and the draft acceptance.
+__device__ __forceinline__ void entropy_stage_b(const EntropyParams &P, int row, int G, int k, EntStageB &b,
+                                                EntLds &sl) {
+    const int tid = threadIdx.x;
+    const int n = row_merge(P.g_key, P.g_val, P.g_cnt, row, G, k, b.ml, b.okey, b.oval);
+    double &s_M = sl.M, &s_Z = sl.Z;
     if (tid == 0) {
         const double *gs = P.g_stat + (int64_t)row * G * 3;
         double Mr = -INFINITY;
@@ -134,16 +162,90 @@ __global__ __launch_bounds__(kThreads) void entropy_kernel(EntropyParams P) {
         s_M = Mr;
         s_Z = Z;
         if (P.entropy) P.entropy[row] = (float)(log(Z) - A / Z);
-        uint32_t am = n > 0 ? ckey_id(sm.b.okey[0]) : 0u;
+        uint32_t am = n > 0 ? ckey_id(b.okey[0]) : 0u;
         if (P.argmax) P.argmax[row] = am;
         if (P.accept && P.draft) P.accept[row] = (uint8_t)(am == P.draft[row]);
     }
     __syncthreads();
     if (tid < n) {
         int64_t o = (int64_t)row * P.out_ld + tid;
-        if (P.ids) P.ids[o] = ckey_id(sm.b.okey[tid]);
-        if (P.probs) P.probs[o] = (float)(exp((double)sm.b.oval[tid] - s_M) / s_Z);
+        if (P.ids) P.ids[o] = ckey_id(b.okey[tid]);
+        if (P.probs) P.probs[o] = (float)(exp((double)b.oval[tid] - s_M) / s_Z);
     }
+}
+
+// Batches whose chunked grid would take more than one round of workgroups
+// (config 4: 64 rows x 8 chunks at one workgroup per CU): G segments per row,
+// each walked by one workgroup in steps of what its registers hold.  The next
+// step's loads are requested while this step is selected, the workgroup's
+// top-k so far is kept sorted in LDS, and once it holds k entries its k-th
+// value is the step's threshold (no threshold sort).  The segment's list and
+// (max, S, U) record then take the chunked kernel's handoff and stage B.
+template <typename T, int NV>
+__global__ __launch_bounds__(kThreads) void entropy_walk_kernel(EntropyParams P) {
+    __shared__ union {
+        EntStageA<T, NV> a;
+        EntStageB b;
+    } sm;
+    __shared__ RowLoopLds rl;
+    __shared__ uint32_t s_bins[256];
+    __shared__ uint32_t s_tau[1];
+    __shared__ int s_dig[2];
+    __shared__ int s_n, s_flag;
+    __shared__ EntLds sl;
+
+    constexpr int VEC = VecTraits<T>::VEC;
+    constexpr int SUB = kThreads * NV * VEC;
+    const RowSource &a = P.src;
+    const int tid = threadIdx.x;
+    const int G = a.G;
+    const int row = blockIdx.x / G;
+    const int g = blockIdx.x - row * G;
+    const int s0 = g * a.CH;
+    const int s1 = min(a.V, s0 + a.CH);
+    const int k = P.k;
+
+    float ref = -INFINITY, S = 0.0f, U = 0.0f;
+    int n_run = 0, cur = 0;
+    uint4 pf[NV];
+    chunk_request<T, NV>(a, row, s0, min(s1, s0 + SUB), pf);
+    for (int c0 = s0; c0 < s1; c0 += SUB) {
+        const int c1 = min(s1, c0 + SUB);
+        ChunkRegs<T, NV> cr;
+        chunk_stream<T, NV, false, false, false, EntHook, NV, NoMid, true>(
+            a, row, c0, c1, cr, nullptr, nullptr, EntHook{&ref, &S, &U}, NoMid(), pf, c1, min(s1, c1 + SUB));
+        float tau;
+        if (n_run == k) {  // uniform: nothing below the running k-th value can enter
+            if (tid == 0) s_n = 0;
+            if (tid < kSortMax) sm.a.sel.rank[tid] = 0u;
+            __syncthreads();
+            tau = okey_inv((uint32_t)(rl.key[cur][k - 1] >> 32));
+        } else {
+            tau = select_prepare<T, NV>(cr.lmax, k, sm.a.sel, s_tau, &s_n);
+        }
+        chunk_select_publish<T, NV, false, true>(a, cr, c0, k, sm.a.sel, nullptr, nullptr, s_tau, &s_n, s_bins,
+                                                 s_dig, ChunkOut{rl.bk, rl.bv, &rl.bn}, tau);
+        __syncthreads();  // the step's list is in rl.bk / rl.bv / rl.bn
+        running_merge(rl, cur, n_run, k);
+    }
+    const int64_t rg = (int64_t)row * G + g;
+    ent_stats_reduce(ref, S, U, sl);
+    if (tid < k) {  // the segment's list, zero-padded to k like a chunk's
+        st_agent(&P.g_key[rg * kCapA + tid], tid < n_run ? rl.key[cur][tid] : (uint64_t)0);
+        if (tid < n_run) st_agent(&P.g_val[rg * kCapA + tid], rl.val[cur][tid]);
+    }
+    if (tid == 0) st_agent(P.g_cnt + rg, n_run);
+    __syncthreads();  // per-wave sums of the record
+    ent_stats_publish(P, rg, sl);
+    if (!row_ticket(P.tickets, row, G, &s_flag)) return;
+    entropy_stage_b(P, row, G, k, sm.b, sl);
+}
+
+hipError_t launch_entropy_walk(const EntropyParams &P, int dtype, int rows, hipStream_t st) {
+    dim3 grid(rows * P.src.G), block(kThreads);
+    if (dtype == 0) hipLaunchKernelGGL((entropy_walk_kernel<float, 8>), grid, block, 0, st, P);
+    else hipLaunchKernelGGL((entropy_walk_kernel<uint16_t, 4>), grid, block, 0, st, P);
+    return hipGetLastError();
 }
 
 template <typename T, int NV>

@@ -145,6 +145,8 @@ hipError_t launch_nucleus_capped(const SampleParams &P, int dtype, int nv, int r
 hipError_t launch_exact(const ExactParams &P, int dtype, int rows, hipStream_t st);
 hipError_t launch_argmax(const ArgmaxParams &P, int dtype, int nv, int rows, hipStream_t st);
 hipError_t launch_entropy(const EntropyParams &P, int dtype, int nv, int rows, hipStream_t st);
+// G segments per row, each walked by one workgroup (entropy_walk_kernel).
+hipError_t launch_entropy_walk(const EntropyParams &P, int dtype, int rows, hipStream_t st);
 hipError_t launch_mask(const MaskParams &P, hipStream_t st);
 // Copies each row's penalty window (the last min(hist_len, win) ids) to
 // out[row][0, nw) and nw to out_len[row] (rows with hist_ld > kMaxWinHost).

@@ -1034,6 +1034,56 @@ __device__ __forceinline__ void chunk_select_late(const RowSource &a, int row, C
     chunk_select_publish<T, NV, false>(a, cr, c0, k, sl, nullptr, nullptr, s_tau, s_n, bins, s_dig, out);
 }
 
+// ------------------------------------------- running list of a walking workgroup
+// A workgroup that walks several chunks keeps its top-k so far sorted in LDS
+// (double-buffered); each chunk publishes its own list to bk / bv / bn.
+struct RowLoopLds {
+    uint64_t key[2][kCapA];  // running list, double-buffered
+    float val[2][kCapA];
+    uint64_t bk[kCapA];      // this chunk's list
+    float bv[kCapA];
+    int32_t bn;
+};
+
+// Entries of the sorted-descending list L[0, n) greater than `mine`.
+__device__ __forceinline__ int count_greater_n(const uint64_t *L, int n, uint64_t mine) {
+    int lo = 0, hi = n;  // L[i] > mine for i < lo, L[i] <= mine for i >= hi
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (L[mid] > mine) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
+
+// Merges the chunk's list (bk, bv, bn; after a barrier) into the running list
+// by rank: each entry binary-searches the other list and writes itself to its
+// rank in the other buffer.  Ends with a barrier.
+__device__ __forceinline__ void running_merge(RowLoopLds &rl, int &cur, int &n_run, int k) {
+    const int tid = threadIdx.x;
+    const int nb = rl.bn;
+    const int nxt = cur ^ 1;
+    if (tid < n_run) {
+        const uint64_t mine = rl.key[cur][tid];
+        const int r = tid + count_greater_n(rl.bk, nb, mine);
+        if (r < k) {
+            rl.key[nxt][r] = mine;
+            rl.val[nxt][r] = rl.val[cur][tid];
+        }
+    } else if (tid >= kCapA && tid - kCapA < nb) {
+        const int i = tid - kCapA;
+        const uint64_t mine = rl.bk[i];
+        const int r = i + count_greater_n(rl.key[cur], n_run, mine);
+        if (r < k) {
+            rl.key[nxt][r] = mine;
+            rl.val[nxt][r] = rl.bv[i];
+        }
+    }
+    n_run = min(k, n_run + nb);
+    cur = nxt;
+    __syncthreads();  // the running list is complete; stage-A LDS may be reused
+}
+
 // ------------------------------------------------------------- stage B
 // Loads the G sorted chunk lists of a row (one round trip: every slot is
 // requested before any is used; every list holds k slots, padded with key 0)

@@ -240,13 +240,6 @@ __global__ __launch_bounds__(kThreads) void nucleus_kernel(SampleParams P) {
 // distinct: each holds the count of greater entries of the other list by a
 // binary search).  NUC: the prefix pass of whole-vocabulary rows, with the
 // row total accumulated over the chunks in each thread.
-struct RowLoopLds {
-    uint64_t key[2][kCapA];  // running list, double-buffered
-    float val[2][kCapA];
-    uint64_t bk[kCapA];      // this chunk's list
-    float bv[kCapA];
-    int32_t bn;
-};
 
 // The whole-vocabulary prefix threshold for min_p > 0: an entry below it has
 // exp(x - M) < min_p for every maximum >= M, with room for the f32 rounding of
@@ -258,16 +251,6 @@ __device__ __forceinline__ float minp_floor(float M, double ln_minp) {
     return t;
 }
 
-// Entries of the sorted-descending list L[0, n) greater than `mine`.
-__device__ __forceinline__ int count_greater_n(const uint64_t *L, int n, uint64_t mine) {
-    int lo = 0, hi = n;  // L[i] > mine for i < lo, L[i] <= mine for i >= hi
-    while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        if (L[mid] > mine) lo = mid + 1;
-        else hi = mid;
-    }
-    return lo;
-}
 
 template <typename T, int NV, bool HAS_MASK, bool HAS_PEN, bool NUC, bool BY_MAX, bool CAP>
 __global__ __launch_bounds__(kThreads) void row_kernel(SampleParams P) {
@@ -376,27 +359,7 @@ __global__ __launch_bounds__(kThreads) void row_kernel(SampleParams P) {
             }
         }
         __syncthreads();  // the chunk's list is in rl.bk / rl.bv / rl.bn
-        const int nb = rl.bn;
-        const int nxt = cur ^ 1;
-        if (tid < n_run) {
-            const uint64_t mine = rl.key[cur][tid];
-            const int r = tid + count_greater_n(rl.bk, nb, mine);
-            if (r < k) {
-                rl.key[nxt][r] = mine;
-                rl.val[nxt][r] = rl.val[cur][tid];
-            }
-        } else if (tid >= kCapA && tid - kCapA < nb) {
-            const int i = tid - kCapA;
-            const uint64_t mine = rl.bk[i];
-            const int r = i + count_greater_n(rl.key[cur], n_run, mine);
-            if (r < k) {
-                rl.key[nxt][r] = mine;
-                rl.val[nxt][r] = rl.bv[i];
-            }
-        }
-        n_run = min(k, n_run + nb);
-        cur = nxt;
-        __syncthreads();  // the running list is complete; stage-A LDS may be reused
+        running_merge(rl, cur, n_run, k);
     }
 
     double tot = -1.0;
