@@ -66,6 +66,15 @@ def copy_calibration(nbytes: int = 256 * 2**20, reps: int = 8):
     print(json.dumps({"copy_calibration_bytes": nbytes, "reps": reps}), flush=True)
 
 
+def _entropy_chunks(V: int, rows: int) -> int:
+    """Chunks per row of the chunked entropy plan (zi::plan_rows, f32)."""
+    ept = 64
+    chunks = lambda e: -(-V // (512 * e))
+    while ept > 16 and rows * chunks(ept) < 256 and chunks(ept // 2) <= 8:
+        ept //= 2
+    return chunks(ept)
+
+
 def read_traffic(path: str, kernel: str, workload: str):
     """HBM bytes per launch from a committed rocprofv3 --pmc summary line:
     `traffic <workload> <kernel> <bytes>`."""
@@ -449,7 +458,10 @@ def bench_entropy(args, w):
                    "launch": "hip_graph_replay"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "algorithmic_bytes_per_launch": nbytes, "kernel": "entropy_kernel"},
+                     "algorithmic_bytes_per_launch": nbytes,
+                     # batches whose chunked grid exceeds one workgroup per CU walk their segments
+                     "kernel": "entropy_walk_kernel" if w.rows * _entropy_chunks(w.vocab, w.rows) > 256
+                     else "entropy_kernel"},
         "cpu_baseline": cpu,
         "wall_s": round(wall, 3),
     }), flush=True)
