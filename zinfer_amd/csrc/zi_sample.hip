@@ -328,6 +328,11 @@ __global__ __launch_bounds__(kThreads) void row_kernel(SampleParams P) {
                 }
             }
             tau = m_run == -INFINITY ? -INFINITY : fminf(minp_floor(m_run, ln_minp), m2_run);
+        } else if (n_run == k) {  // uniform: nothing below the running k-th value can enter
+            if (tid == 0) s_n = 0;
+            if (tid < kSortMax) sm.a.sel.rank[tid] = 0u;
+            __syncthreads();
+            tau = -INFINITY;
         } else {
             tau = select_prepare<T, NV>(cr.lmax, k, sm.a.sel, s_tau, &s_n);
         }
