@@ -29,6 +29,9 @@ def _rows(rng, kind, rows, V):
         return np.full((rows, V), 1.5, np.float32)
     if kind == "allneginf":  # every candidate -inf: the reference falls back to c[n-1]
         return np.full((rows, V), -np.inf, np.float32)
+    if kind == "rising":  # increasing along the row: every later step beats the running top-k
+        ramp = np.linspace(-6.0, 6.0, V, dtype=np.float32)
+        return (ramp[None, :] + rng.standard_normal((rows, V)).astype(np.float32) * 0.01).astype(np.float32)
     raise ValueError(kind)
 
 
@@ -145,6 +148,8 @@ def test_long_history_rows(ctx, oracle, H, win):
     (260, 131072, 256, "normal", True, False),
     (256, 4099, 7, "ints", True, True),
     (512, 17, 5, "flat", False, False),
+    (256, 70000, 50, "rising", True, False),
+    (256, 40000, 256, "rising", False, False),
 ])
 def test_large_batch_rows(ctx, oracle, rows, V, k, kind, pen, mask):
     """Batches of >= 256 rows run one workgroup per row (the running top-k
