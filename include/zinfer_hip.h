@@ -69,8 +69,10 @@ typedef struct zi_params {
     uint64_t seed;               /* 0    (host Sampler RNG seed) */
     float    final_logit_softcap; /* 0   (0 = off) cap*tanh(l/cap) on each logit before the mask, the
                                      model's epilogue (src/model.zig:2492-2514) fused into the read;
-                                     set it when the producer leaves logits uncapped.  V must be a
-                                     multiple of 32 (the reference's scalar tail is not restated). */
+                                     set it when the producer leaves logits uncapped.  Ids below
+                                     32*floor(V/32) take the reference's vector body (tanh through
+                                     exp, clamped at |l/cap| = 9), the rest its scalar tail
+                                     (cap * tanh(l / cap)). */
 } zi_params;
 
 /* Fills the reference defaults (src/sampler.zig:4-26). */

@@ -15,6 +15,10 @@
 
 float or_exp32(float x) { return (float)exp((double)x); }
 float or_log32(float x) { return (float)log((double)x); }
+/* std.math.tanh(f32) (model.zig:2512, the softcap's scalar tail), as the f64
+ * tanh rounded once to f32: within half an ulp plus the f64 error, the same
+ * footing as or_exp32. */
+float or_tanh32(float x) { return (float)tanh((double)x); }
 
 /* std.math.pow(f32, x, y) as Zig computes it (src/sampler.zig:182 calls it for
  * the DRY penalty).  Zig's lib/std/math/pow.zig (Zig 0.17.1, not in the
@@ -99,6 +103,11 @@ void or_params_default(or_params *p) {
  * i < 32*floor(V/32)): z = l * (1/cap) with 1/cap in f32, clamped to [-9, 9],
  * e = exp(2z), tanh = (e - 1) / (e + 1), l = cap * tanh.  Every sequence step
  * rounds to f32; exp is or_exp32. */
+/* The scalar tail of the same loop (model.zig:2511-2513, ids >= 32*floor(V/32)):
+ * l = cap * tanh(l / cap), a true division and no clamp, so -inf maps to -cap
+ * (the body maps it to -cap*tanh(9)). */
+float or_softcap_tail(float l, float cap) { return cap * or_tanh32(l / cap); }
+
 float or_softcap(float l, float cap) {
     const float inv_cap = 1.0f / cap;
     /* @min(@max(z, -9), 9) lowers to maxnum/minnum: a NaN operand yields the other */
@@ -433,9 +442,8 @@ or_result or_sample_row(const or_params *p, float *logits, uint32_t V, const uin
         const float cap = p->final_logit_softcap;
         const uint32_t body = V / 32 * 32;
         for (uint32_t i = 0; i < body; ++i) logits[i] = or_softcap(logits[i], cap);
-        /* the scalar tail calls std.math.tanh (:2511-2513), restated here with libm's tanhf:
-         * PARITY UNPINNED (no Zig); the product rejects V not a multiple of 32 */
-        for (uint32_t i = body; i < V; ++i) logits[i] = cap * tanhf(logits[i] / cap);
+        /* the scalar tail, ids >= 32*floor(V/32) (:2511-2513) */
+        for (uint32_t i = body; i < V; ++i) logits[i] = or_softcap_tail(logits[i], cap);
     }
     if (mask) or_apply_mask(logits, V, mask); /* gen.zig:457-460: mask precedes sample */
     or_apply_penalty(logits, V, window, n_window, p->repeat_penalty, p->freq_penalty,

@@ -37,13 +37,28 @@
  *                          accepted to the finished state parses with json.loads;
  *                          hand-derived byte tables per state (the \\u quirk, the
  *                          depth-64 limit, object-only roots).
- *   or_rng_*               PARITY UNPINNED for the Zig DefaultPrng stream (no Zig
- *                          here, no reference vectors); splitmix64 alone is pinned
- *                          by its published sequence for seed 1234567.
- *   exp                    Zig @exp (compiler-rt expf) last-ulp bits are PARITY
- *                          UNPINNED; both this oracle and the device tail use
- *                          or_exp32 = (float)exp((double)x), correctly rounded in
- *                          practice.
+ *   or_xoshiro_*           linear engine pinned (tests/test_oracle_rng.py): the
+ *                          GF(2) update matrix has full period 2^256 - 1 (checked
+ *                          against every prime of 2^256 - 1) and reproduces the
+ *                          published JUMP / LONG_JUMP polynomials (2^128 and 2^192
+ *                          steps); seeding by splitmix64 is pinned by splitmix64's
+ *                          published sequence for seed 1234567.  The ++ output
+ *                          scrambler rotl(s0 + s3, 23) + s0 is PARITY UNPINNED (no
+ *                          Zig and no published output vectors here).
+ *   or_rand_f32            pinned: crafted states with chosen outputs give
+ *                          2^-(1+lz) * (1 + m/2^23) (m = low 23 bits of the first
+ *                          draw; lz extended by the second draw from 41 leading
+ *                          zeros on), computed independently with ldexp.  The
+ *                          third-draw branch (probability 2^-105) is unpinned.
+ *   or_softcap             pinned: within cap*2^-22 of the f64 closed form, odd,
+ *                          saturation and special values.
+ *   or_softcap_tail        pinned: within two f32 ulps of cap*tanh(fl(l/cap)) in f64,
+ *                          odd, +-inf -> +-cap, and applied to exactly the ids at
+ *                          and above 32*floor(V/32) (tests/test_oracle_properties.py).
+ *   exp, tanh              Zig @exp (compiler-rt expf) and std.math.tanh last-ulp
+ *                          bits are PARITY UNPINNED; this oracle and the device use
+ *                          (float)exp((double)x) and (float)tanh((double)x),
+ *                          correctly rounded in practice.
  */
 #ifndef ZINFER_ORACLE_H
 #define ZINFER_ORACLE_H
@@ -96,6 +111,7 @@ typedef struct or_sample_diag {
 
 float or_exp32(float x);
 float or_log32(float x);
+float or_tanh32(float x);
 float or_pow_zig(float x, float y);
 
 void or_params_default(or_params *p);
@@ -188,8 +204,10 @@ typedef struct or_json {
     uint8_t pad_;
 } or_json;
 
-/* model.zig:2492-2510 final-logit softcap, vectorized-body formula. */
+/* model.zig:2492-2510 final-logit softcap, vectorized-body formula, and the
+ * scalar tail (:2511-2513) for ids >= 32*floor(V/32). */
 float  or_softcap(float l, float cap);
+float  or_softcap_tail(float l, float cap);
 
 void   or_json_init(or_json *j, int object_only);
 int    or_json_is_finished(const or_json *j);

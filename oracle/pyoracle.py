@@ -101,6 +101,10 @@ def lib():
         L.or_softcap.argtypes = [C.c_float, C.c_float]
         L.or_exp32.restype = C.c_float
         L.or_exp32.argtypes = [C.c_float]
+        L.or_tanh32.restype = C.c_float
+        L.or_tanh32.argtypes = [C.c_float]
+        L.or_softcap_tail.restype = C.c_float
+        L.or_softcap_tail.argtypes = [C.c_float, C.c_float]
         L.or_pow_zig.restype = C.c_float
         L.or_pow_zig.argtypes = [C.c_float, C.c_float]
         L.or_params_default.argtypes = [C.POINTER(OrParams)]
@@ -168,6 +172,14 @@ def params(**kw) -> OrParams:
 
 def softcap(x: float, cap: float) -> float:
     return lib().or_softcap(float(x), float(cap))
+
+
+def softcap_tail(x: float, cap: float) -> float:
+    return lib().or_softcap_tail(float(x), float(cap))
+
+
+def tanh32(x: float) -> float:
+    return lib().or_tanh32(float(x))
 
 
 def exp32(x: float) -> float:
@@ -277,6 +289,20 @@ def rng_floats(seed: int, n: int):
     s = (C.c_uint64 * 4)()
     lib().or_xoshiro_seed(s, seed)
     return np.array([lib().or_rand_f32(s) for _ in range(n)], dtype=np.float32)
+
+
+def xoshiro_step(state):
+    """One or_xoshiro_next call on the 4-word state: (new state, output)."""
+    s = (C.c_uint64 * 4)(*[int(x) & 0xFFFFFFFFFFFFFFFF for x in state])
+    out = int(lib().or_xoshiro_next(s))
+    return [int(x) for x in s], out
+
+
+def rand_f32_from(state):
+    """or_rand_f32 on the 4-word state: (value, state after the draws)."""
+    s = (C.c_uint64 * 4)(*[int(x) & 0xFFFFFFFFFFFFFFFF for x in state])
+    v = float(lib().or_rand_f32(s))
+    return v, [int(x) for x in s]
 
 
 def bench_sample_rows(p: OrParams, logits2d, hist, hist_len, mask, uniforms, reps: int):

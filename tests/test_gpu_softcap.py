@@ -1,4 +1,4 @@
-"""GPU parity: the final-logit softcap (src/model.zig:2492-2510) fused into the
+"""GPU parity: the final-logit softcap (src/model.zig:2492-2513) fused into the
 batched sampler's read of the logits, vs the CPU oracle that caps the row
 first and then samples it (mask, penalty, edits, sampleWithMargin).
 
@@ -96,23 +96,51 @@ def test_softcap_greedy_matches_oracle(ctx, oracle, V):
     assert not errs, "\n".join(errs[:20])
 
 
-def test_softcap_rejects_ragged_vocab(ctx):
-    """The reference's scalar tail (model.zig:2511-2513, std.math.tanh) is not
-    restated: a vocabulary that is not a multiple of 32 is refused."""
-    from zinfer_amd._lib import ZI_ERR_UNSUPPORTED, ZiError
+RAGGED = [
+    # (rows, V, params): V not a multiple of 32, so ids >= 32*floor(V/32) take the scalar tail
+    (3, 1000, dict(temp=0.8, top_k=40, top_p=0.95, min_p=0.05)),
+    (4, 32001, dict(temp=1.0, top_k=64, top_p=0.9, min_p=0.0)),
+    (2, 151937, dict(temp=0.9, top_k=0, top_p=0.9, min_p=0.0)),
+    (2, 4127, dict(temp=0.7, top_k=1000, top_p=0.98, min_p=0.05)),
+    (256, 20007, dict(temp=0.8, top_k=50, top_p=0.9, min_p=0.05)),
+    (260, 4999, dict(temp=1.0, top_k=0, top_p=0.95, min_p=0.05)),
+    (5, 70023, dict(temp=0.0)),
+]
 
-    x = np.zeros((1, 1000), np.float32)
-    with pytest.raises(ZiError) as ei:
-        gpu_sample(ctx, dict(final_logit_softcap=30.0), x, np.zeros((1, 2), np.float32))
-    assert ei.value.code == ZI_ERR_UNSUPPORTED
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("case", range(len(RAGGED)))
+def test_softcap_ragged_vocab_tail(ctx, oracle, case, bf16):
+    """The reference's scalar tail (model.zig:2511-2513, cap * tanh(l / cap))
+    on the last V mod 32 ids.  The row's leaders sit in the tail and the
+    other tail values are small, where the body's exp form and the tail's
+    tanh round differently, so the sampled candidates carry tail values."""
+    rows, V, pk = RAGGED[case]
+    rng = np.random.Generator(np.random.PCG64(4200 + case))
+    body = V // 32 * 32
+    x = (rng.standard_normal((rows, V)) * 3).astype(np.float32)
+    x[:, body:] = (rng.standard_normal((rows, V - body)) * 1e-3).astype(np.float32)
+    x[:, V - 1] = 25.0  # a tail leader (capped near cap)
+    x[:, body] = 0.25 * (1 + np.arange(rows, dtype=np.float32))
+    if bf16:
+        x = _bf16_round(x)
+    hist = rng.integers(body, V, (rows, 40), dtype=np.uint32)  # penalties on tail ids (owner reloads)
+    hl = rng.integers(0, 41, rows).astype(np.int32)
+    pk = dict(pk, final_logit_softcap=4.0, repeat_penalty=1.2, penalty_last_n=64)
+    u = rng.random((rows, 2), dtype=np.float32)
+    g = gpu_sample(ctx, pk, x, u, hist, hl, bf16=bf16)
+    o = oracle_sample(oracle, pk, x, u, hist, hl)
+    errs = compare_sample(g, o, pk, V, f"softcap ragged case{case}")
+    assert not errs, "\n".join(errs[:20])
 
 
-def test_host_sampler_caps_row_in_place(ctx, oracle):
+@pytest.mark.parametrize("V", [8192, 8197])
+def test_host_sampler_caps_row_in_place(ctx, oracle, V):
     """The host Sampler caps the caller's row in place (what the reference's
-    forward leaves in the logits), then samples and applies the penalty."""
+    forward leaves in the logits, the scalar tail included when V is not a
+    multiple of 32), then samples and applies the penalty."""
     from zinfer_amd.api import Sampler, params
 
-    V = 8192
     pk = dict(temp=0.9, top_k=30, top_p=0.9, min_p=0.02, repeat_penalty=1.3, penalty_last_n=64,
               final_logit_softcap=20.0, seed=99)
     smp = Sampler(ctx, V, params(**pk))

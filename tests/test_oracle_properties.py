@@ -297,6 +297,50 @@ def test_softcap_saturates_and_special_values(oracle):
     assert oracle.softcap(0.0, cap) == 0.0
 
 
+@pytest.mark.parametrize("cap", [30.0, 15.0, 1.0])
+def test_softcap_tail_is_tanh(oracle, cap):
+    """The scalar tail (model.zig:2511-2513) is cap * tanh(l / cap) with no
+    clamp: within two f32 ulps of cap * tanh(fl(l / cap)) in f64 (half an ulp
+    each for the rounded tanh, scaled by cap, and for the product), odd,
+    tanh(+-inf) = +-1, signed zero kept, NaN propagated."""
+    rng = np.random.default_rng(int(cap) + 100)
+    ls = np.concatenate([rng.standard_normal(2000) * cap * 2, rng.standard_normal(500) * 1e-3 * cap,
+                         np.linspace(-12 * cap, 12 * cap, 2001)]).astype(np.float32)
+    got = np.array([oracle.softcap_tail(x, cap) for x in ls], np.float64)
+    q = (ls.astype(np.float64) / cap).astype(np.float32).astype(np.float64)  # fl(l / cap)
+    want = cap * np.tanh(q)
+    ulp = np.spacing(np.abs(want).astype(np.float32)).astype(np.float64)
+    assert np.all(np.abs(got - want) <= 2.0 * ulp + 1e-45)
+    neg = np.array([oracle.softcap_tail(-x, cap) for x in ls], np.float64)
+    assert np.array_equal(neg, -got)
+    assert oracle.softcap_tail(np.inf, cap) == cap and oracle.softcap_tail(-np.inf, cap) == -cap
+    assert np.signbit(oracle.softcap_tail(-0.0, cap)) and oracle.softcap_tail(0.0, cap) == 0.0
+    assert np.isnan(oracle.softcap_tail(float("nan"), cap))
+
+
+def test_softcap_tail_covers_the_last_v_mod_32(oracle):
+    """Only ids >= 32*floor(V/32) take the tail.  Near zero the body's
+    (e^2z - 1)/(e^2z + 1) loses most of its bits to the cancellation in
+    e^2z - 1, the tail does not, so a row of small logits tells the two apart
+    by position: sampling it with the cap matches a row capped with the body
+    formula below 32*floor(V/32) and the tail formula above it."""
+    cap = 30.0
+    for V in (33, 45, 64 + 31, 320):
+        body = V // 32 * 32
+        x = (np.arange(V, dtype=np.float32) + 1.0) * np.float32(1e-3)  # distinct small logits, rising with id
+        capped = np.array([oracle.softcap(v, cap) if i < body else oracle.softcap_tail(v, cap)
+                           for i, v in enumerate(x)], np.float32)
+        tail_vals = np.array([oracle.softcap_tail(v, cap) for v in x[body:]], np.float32)
+        body_vals = np.array([oracle.softcap(v, cap) for v in x[body:]], np.float32)
+        if V > body:
+            assert not np.array_equal(tail_vals, body_vals)  # the formulas differ on these inputs
+        pk = dict(temp=0.7, top_k=0, top_p=1.0, min_p=0.0)
+        _, _, d1 = oracle.sample_row(oracle.params(final_logit_softcap=cap, **pk), x, [0.5, 0.5], cap=V)
+        _, _, d2 = oracle.sample_row(oracle.params(**pk), capped, [0.5, 0.5], cap=V)
+        assert np.array_equal(d1["row"], capped)  # the row as the sampler saw it
+        assert np.array_equal(d1["ids"], d2["ids"]) and np.array_equal(d1["vals"], d2["vals"])
+
+
 @pytest.mark.parametrize("seed", range(4))
 def test_softcap_precedes_mask_and_penalty(oracle, seed):
     """The cap belongs to the forward (model.zig:2492), so it runs before the

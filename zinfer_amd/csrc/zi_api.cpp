@@ -197,11 +197,9 @@ static int32_t fill_source(const zi_batch *b, const zi_params *p, bool with_inpu
         s.mask_ld = b->mask_ld;
     }
     if (p && p->final_logit_softcap > 0.0f) {
-        if (b->vocab % 32)
-            return zi_fail(ZI_ERR_UNSUPPORTED, "%s: final_logit_softcap with V=%d (not a multiple of 32)", fn,
-                           b->vocab);
         s.cap = p->final_logit_softcap;
         s.inv_cap = 1.0f / p->final_logit_softcap;
+        s.cap_body = b->vocab / 32 * 32;  // the reference's vector body; the rest is its scalar tail
     }
     if (p) {
         s.rp = p->repeat_penalty;
@@ -232,8 +230,31 @@ static int32_t fill_source(const zi_batch *b, const zi_params *p, bool with_inpu
     return ZI_OK;
 }
 
-static int32_t run_argmax(zi_ctx *c, const zi::RowSource &src, const zi_batch *b, const zi::Plan &pl,
-                          uint32_t *tok, float *margin, uint32_t *tok_low, float *margin_true, int32_t *ndraws) {
+namespace {
+// The device scratch one call works in: a context's buffers, or the static
+// array of zi_sample_rows_noalloc.  Layouts: zi_launch.hpp.
+struct Scratch {
+    uint64_t *g_key;
+    float *g_val;
+    int32_t *g_cnt;
+    int32_t *tickets;
+    uint64_t *g_cls;
+    uint32_t *g_raw;
+    float *g_top2;
+    float *g_tail;
+    uint32_t *win_ids;  // NULL: no window compaction (histories up to kMaxWinHost wide only)
+    int32_t *win_len;
+};
+
+Scratch ctx_scratch(const zi_ctx *c) {
+    return Scratch{c->g_key, c->g_val, c->g_cnt, c->tickets, c->g_cls, c->g_raw, c->g_top2, c->g_tail,
+                   c->win_ids, c->win_len};
+}
+}  // namespace
+
+static int32_t run_argmax(const Scratch &S, hipStream_t st, const zi::RowSource &src, const zi_batch *b,
+                          const zi::Plan &pl, uint32_t *tok, float *margin, uint32_t *tok_low, float *margin_true,
+                          int32_t *ndraws) {
     zi::ArgmaxParams P;
     std::memset(&P, 0, sizeof P);
     P.src = src;
@@ -242,12 +263,12 @@ static int32_t run_argmax(zi_ctx *c, const zi::RowSource &src, const zi_batch *b
     P.tok_low = tok_low;
     P.margin_true = margin_true;
     P.ndraws = ndraws;
-    P.g_cls = c->g_cls;
-    P.g_raw = c->g_raw;
-    P.g_top2 = c->g_top2;
-    P.g_tail = c->g_tail;
-    P.tickets = c->tickets;
-    hipError_t e = zi::launch_argmax(P, b->dtype, pl.nv, b->rows, c->stream);
+    P.g_cls = S.g_cls;
+    P.g_raw = S.g_raw;
+    P.g_top2 = S.g_top2;
+    P.g_tail = S.g_tail;
+    P.tickets = S.tickets;
+    hipError_t e = zi::launch_argmax(P, b->dtype, pl.nv, b->rows, st);
     if (e != hipSuccess) return zi_hip_fail(e, "argmax kernel launch");
     return ZI_OK;
 }
@@ -339,35 +360,38 @@ static int32_t run_whole_order(zi_ctx *c, const zi_params *p, const zi_batch *b,
     return ZI_OK;
 }
 
-extern "C" int32_t zi_sample_rows(zi_ctx *c, const zi_params *p, const zi_batch *b, const float *uniforms,
-                                  const zi_sample_out *out) {
-    int32_t rc = check_batch(c, b, "zi_sample_rows");
-    if (rc) return rc;
-    if (!p || !out || !out->tok || !out->margin)
-        return zi_fail(ZI_ERR_INVALID, "zi_sample_rows: NULL params/out/tok/margin");
-    HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+// zi_sample_rows after the batch checks, on scratch S and stream st.  c (for
+// the whole-order path's lazily allocated sort scratch) may be NULL: top_k
+// resolving to more than kMaxTopK is then refused.
+static int32_t sample_core(zi_ctx *c, const Scratch &S, hipStream_t st, const zi_params *p, const zi_batch *b,
+                           const float *uniforms, const zi_sample_out *out, const char *fn) {
     const zi::Plan pl = zi::plan_rows(b->rows, b->vocab, b->dtype);
     zi::RowSource src;
-    rc = fill_source(b, p, true, src, pl, "zi_sample_rows");
+    int32_t rc = fill_source(b, p, true, src, pl, fn);
     if (rc) return rc;
     if (src.hist && src.hist_ld > zi::kMaxWinHost) {  // the kernels prefetch whole history rows
-        hipError_t e = zi::launch_window_compact(src.hist, src.hist_len, src.hist_ld, src.win, b->rows, c->win_ids,
-                                                 c->win_len, c->stream);
+        if (!S.win_ids)
+            return zi_fail(ZI_ERR_UNSUPPORTED, "%s: hist_ld %d > %d", fn, src.hist_ld, zi::kMaxWinHost);
+        hipError_t e = zi::launch_window_compact(src.hist, src.hist_len, src.hist_ld, src.win, b->rows, S.win_ids,
+                                                 S.win_len, st);
         if (e != hipSuccess) return zi_hip_fail(e, "window compaction launch");
-        src.hist = c->win_ids;
-        src.hist_len = c->win_len;
+        src.hist = S.win_ids;
+        src.hist_len = S.win_len;
         src.hist_ld = zi::kMaxWinHost;
     }
 
     if (p->temp <= 0.0f)  // greedy: argmax of the penalized row (src/sampler.zig:193)
-        return run_argmax(c, src, b, pl, out->tok, out->margin, nullptr, nullptr, out->ndraws);
+        return run_argmax(S, st, src, b, pl, out->tok, out->margin, nullptr, nullptr, out->ndraws);
 
-    if (!uniforms) return zi_fail(ZI_ERR_INVALID, "zi_sample_rows: uniforms is NULL");
+    if (!uniforms) return zi_fail(ZI_ERR_INVALID, "%s: uniforms is NULL", fn);
     const uint32_t V = (uint32_t)b->vocab;
     const uint32_t k = (p->top_k == 0 || p->top_k > V) ? V : p->top_k;  // src/sampler.zig:197
-    if (k > (uint32_t)zi::kMaxTopK) return run_whole_order(c, p, b, src, pl, k, uniforms, out);
+    if (k > (uint32_t)zi::kMaxTopK) {
+        if (!c) return zi_fail(ZI_ERR_UNSUPPORTED, "%s: top_k resolves to %u > %d", fn, k, zi::kMaxTopK);
+        return run_whole_order(c, p, b, src, pl, k, uniforms, out);
+    }
     if ((out->cand_ids || out->cand_vals || out->probs) && out->cand_ld < (int32_t)k)
-        return zi_fail(ZI_ERR_INVALID, "zi_sample_rows: cand_ld=%d < k=%u", out->cand_ld, k);
+        return zi_fail(ZI_ERR_INVALID, "%s: cand_ld=%d < k=%u", fn, out->cand_ld, k);
 
     zi::SampleParams P;
     std::memset(&P, 0, sizeof P);
@@ -388,13 +412,23 @@ extern "C" int32_t zi_sample_rows(zi_ctx *c, const zi_params *p, const zi_batch 
     P.cand_vals = out->cand_vals;
     P.probs = out->probs;
     P.cand_ld = out->cand_ld;
-    P.g_key = c->g_key;
-    P.g_val = c->g_val;
-    P.g_cnt = c->g_cnt;
-    P.tickets = c->tickets;
-    hipError_t e = zi::launch_sample(P, b->dtype, pl.nv, b->rows, c->stream);
+    P.g_key = S.g_key;
+    P.g_val = S.g_val;
+    P.g_cnt = S.g_cnt;
+    P.tickets = S.tickets;
+    hipError_t e = zi::launch_sample(P, b->dtype, pl.nv, b->rows, st);
     if (e != hipSuccess) return zi_hip_fail(e, "sample kernel launch");
     return ZI_OK;
+}
+
+extern "C" int32_t zi_sample_rows(zi_ctx *c, const zi_params *p, const zi_batch *b, const float *uniforms,
+                                  const zi_sample_out *out) {
+    int32_t rc = check_batch(c, b, "zi_sample_rows");
+    if (rc) return rc;
+    if (!p || !out || !out->tok || !out->margin)
+        return zi_fail(ZI_ERR_INVALID, "zi_sample_rows: NULL params/out/tok/margin");
+    HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+    return sample_core(c, ctx_scratch(c), c->stream, p, b, uniforms, out, "zi_sample_rows");
 }
 
 extern "C" int32_t zi_sample_rows_pruned(zi_ctx *c, const zi_params *p, const zi_batch *b, const uint32_t *groups,
@@ -494,7 +528,8 @@ extern "C" int32_t zi_argmax_rows(zi_ctx *c, const zi_batch *b, uint32_t *out_to
     zi::RowSource src;
     rc = fill_source(b, nullptr, false, src, pl, "zi_argmax_rows");
     if (rc) return rc;
-    return run_argmax(c, src, b, pl, out_tok, out_margin, out_tok_low, out_margin_true, nullptr);
+    return run_argmax(ctx_scratch(c), c->stream, src, b, pl, out_tok, out_margin, out_tok_low, out_margin_true,
+                      nullptr);
 }
 
 static constexpr int kWalkGroups = 256;  // one workgroup per CU
@@ -562,3 +597,4 @@ extern "C" int32_t zi_apply_mask_rows(zi_ctx *c, const zi_batch *b) {
     if (e != hipSuccess) return zi_hip_fail(e, "mask kernel launch");
     return ZI_OK;
 }
+

@@ -51,6 +51,11 @@ __device__ __forceinline__ float softcap_f(float l, float cap, float inv_cap) {
     return cap * ((e2z - 1.0f) / (e2z + 1.0f));
 }
 
+// The softcap's scalar tail (src/model.zig:2511-2513), ids >= 32*floor(V/32):
+// l = cap * tanh(l / cap) with a true division and no clamp; tanh is the f64
+// tanh rounded once to f32, as in the CPU oracle.
+__device__ __forceinline__ float softcap_tail_f(float l, float cap) { return cap * (float)tanh((double)(l / cap)); }
+
 __device__ __forceinline__ int lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0)); }
 
 // Number of set bits of `m` below this lane.

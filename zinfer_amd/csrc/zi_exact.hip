@@ -91,7 +91,7 @@ __device__ __forceinline__ void exact_vector(const RowSource &a, int row, const 
     unpack<T>(*reinterpret_cast<const uint4 *>(base + id0), v);
     if constexpr (CAP) {
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) v[e] = softcap_f(v[e], a.cap, a.inv_cap);
+        for (int e = 0; e < VEC; ++e) v[e] = softcap_at(a, id0 + e, v[e]);
     }
     if (HAS_MASK) {
         const uint32_t mb = a.mask[(int64_t)row * a.mask_ld + (id0 >> 5)] >> (id0 & 31);

@@ -63,16 +63,19 @@ struct Xoshiro {
     }
 };
 
-// The final-logit softcap of src/model.zig:2492-2510 on a host row, in place
+// The final-logit softcap of src/model.zig:2492-2513 on a host row, in place
 // (the caller's logits then hold what the reference's forward leaves there).
-// Same f32 steps as the device's; V must be a multiple of 32.
+// Same f32 steps as the device's: the vector body below 32*floor(V/32), the
+// scalar tail cap * tanh(l / cap) from there on.
 static void host_softcap(float *logits, uint32_t V, float cap) {
     const float inv_cap = 1.0f / cap;
-    for (uint32_t i = 0; i < V; ++i) {
+    const uint32_t body = V / 32 * 32;
+    for (uint32_t i = 0; i < body; ++i) {
         const float z = std::fmin(std::fmax(logits[i] * inv_cap, -9.0f), 9.0f);
         const float e2z = (float)std::exp((double)(z * 2.0f));
         logits[i] = cap * ((e2z - 1.0f) / (e2z + 1.0f));
     }
+    for (uint32_t i = body; i < V; ++i) logits[i] = cap * (float)std::tanh((double)(logits[i] / cap));
 }
 
 // src/sampler.zig:91-100 plus the frequency/presence extension, on a host row.
@@ -301,8 +304,6 @@ extern "C" int32_t zi_sampler_sample_with_margin(zi_sampler *s, float *logits, u
     if (p.final_logit_softcap > 0.0f) {
         // the caller's row is capped in place, as the reference's forward
         // leaves it, so the device samples it with the cap off
-        if (n % 32)
-            return zi_fail(ZI_ERR_UNSUPPORTED, "final_logit_softcap with vocab %u (not a multiple of 32)", n);
         host_softcap(logits, n, p.final_logit_softcap);
         p.final_logit_softcap = 0.0f;
     }

@@ -16,6 +16,7 @@ constexpr int kMaxEditsHost = 128;  // sparse edits per row
 constexpr int kMaxTopK = 256;
 constexpr int kMaxEntropyK = 64;
 constexpr int kMaxGroupsHost = 1024;  // listed groups of 8 per pruned row (the reference keeps <= 576)
+constexpr int kRowLoopRowsHost = 256;  // sampling batches this large run one workgroup per row (no list scratch)
 
 struct Plan {
     int G, CH, nv;
@@ -40,6 +41,7 @@ struct RowSource {
     float rp, freq, pres;
     int do_rep, do_fp;
     float cap, inv_cap;  // final-logit softcap (cap > 0), applied first
+    int cap_body;        // ids below 32*floor(V/32) take the softcap's vector body, the rest its scalar tail
 };
 
 struct SampleParams {

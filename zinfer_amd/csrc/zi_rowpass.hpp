@@ -64,6 +64,12 @@ __device__ __forceinline__ bool row_ticket(int32_t *tickets, int row, int G, int
     return *s_flag != 0;
 }
 
+// The final-logit softcap of logit `id` (src/model.zig:2492-2513): the vector
+// body below cap_body, the scalar tail from there on.
+__device__ __forceinline__ float softcap_at(const RowSource &a, int id, float v) {
+    return id < a.cap_body ? softcap_f(v, a.cap, a.inv_cap) : softcap_tail_f(v, a.cap);
+}
+
 // --------------------------------------------------------- penalty table
 struct PenTable {
     uint32_t bits[kMaxCH / 32];
@@ -231,7 +237,7 @@ __device__ __forceinline__ void pen_mark(const RowSource &a, PenTable &t, const 
     for (int u = 0; u < kOwnSlots; ++u) {
         if (own.id[u] != 0xFFFFFFFFu) {
             float v = load_logit<T>(row, own.id[u]);
-            if constexpr (CAP) v = softcap_f(v, a.cap, a.inv_cap);
+            if constexpr (CAP) v = softcap_at(a, (int)own.id[u], v);
             if (mrow && !((mrow[own.id[u] >> 5] >> (own.id[u] & 31)) & 1u)) v = -INFINITY;
             own.x[u] = v;
         }
@@ -378,7 +384,7 @@ __device__ __forceinline__ float chunk_stream(const RowSource &a, int row, int c
         }
         if constexpr (CAP) {
 #pragma unroll
-            for (int e = 0; e < VEC; ++e) v[e] = softcap_f(v[e], a.cap, a.inv_cap);
+            for (int e = 0; e < VEC; ++e) v[e] = softcap_at(a, id0 + e, v[e]);
         }
         if (HAS_MASK) {
             uint32_t mb = mw[j] >> (id0 & 31);
