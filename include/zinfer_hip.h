@@ -152,6 +152,23 @@ typedef struct zi_sample_out {
 int32_t zi_sample_rows(zi_ctx *ctx, const zi_params *p, const zi_batch *b,
                        const float *uniforms, const zi_sample_out *out);
 
+/* zi_sample_rows without a context and without allocating: for callers that
+ * cannot call hipMalloc (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation).  No counterpart in the reference (its
+ * sampler runs on the host).  Same inputs, outputs and results as
+ * zi_sample_rows; runs on the calling thread's current HIP device, enqueued
+ * on `stream` (a hipStream_t; NULL = the default stream).  Its scratch is one
+ * static device array per GPU (about 7 MB, held until the process ends; its
+ * address is looked up once per device on the first call).  Each call clears
+ * the row tickets with a small kernel on `stream` and keeps nothing else
+ * between calls, but every call on a GPU shares that GPU's array, so calls
+ * that overlap on one GPU (other streams, other threads) race: serialize
+ * them.  Limits, checked before any HIP call: rows <= 512, vocab <= 262144,
+ * top_k resolving to <= 256 when temp > 0 (ZI_ERR_UNSUPPORTED otherwise: the
+ * whole-order sort needs a context's scratch), hist_ld <= 1024. */
+int32_t zi_sample_rows_noalloc(const zi_params *p, const zi_batch *b, const float *uniforms,
+                               const zi_sample_out *out, void *stream);
+
 /* zi_sample_rows on pruned-vocabulary rows.  Replaces the reference's -inf
  * fill of the whole logit row (src/model.zig:2127-2128) plus the full read of
  * it: the pruned lm_head (:2036-2140) computes only its candidate groups of 8

@@ -118,6 +118,8 @@ SIGNATURES = {
     "zi_set_stream": (C.c_int32, [C.c_void_p, C.c_void_p]),
     "zi_sync": (C.c_int32, [C.c_void_p]),
     "zi_last_error": (C.c_char_p, []),
+    "zi_sample_rows_noalloc": (C.c_int32, [C.POINTER(ZiParams), C.POINTER(ZiBatch), C.c_void_p,
+                                           C.POINTER(ZiSampleOut), C.c_void_p]),
     "zi_abi_version": (C.c_int32, []),
     "zi_sample_rows": (C.c_int32, [C.c_void_p, C.POINTER(ZiParams), C.POINTER(ZiBatch), C.c_void_p,
                                     C.POINTER(ZiSampleOut)]),

@@ -6,6 +6,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 
 #include "../../include/zinfer_hip.h"
 #include "zi_internal.hpp"
@@ -598,3 +599,101 @@ extern "C" int32_t zi_apply_mask_rows(zi_ctx *c, const zi_batch *b) {
     return ZI_OK;
 }
 
+// ------------------------------------------------ allocation-free sampling
+// zi_sample_rows_noalloc works in one file-scope device array per GPU instead
+// of a context's hipMalloc'd scratch.  Its layout is a Scratch for up to
+// kNaRows rows: chunk lists for the batches that take the chunked kernel
+// (rows < kRowLoopRowsHost; larger batches run one workgroup per row and keep
+// their lists in LDS), tickets, and the greedy path's per-chunk records.
+namespace {
+constexpr int kNaRows = 512;
+constexpr int kNaListRows = zi::kRowLoopRowsHost - 1;
+constexpr size_t na_align(size_t x) { return (x + 255) & ~(size_t)255; }
+constexpr size_t kNaKeyOff = 0;
+constexpr size_t kNaValOff = kNaKeyOff + na_align((size_t)kNaListRows * zi::kMaxGHost * zi::kCapAHost * 8);
+constexpr size_t kNaCntOff = kNaValOff + na_align((size_t)kNaListRows * zi::kMaxGHost * zi::kCapAHost * 4);
+constexpr size_t kNaTicketOff = kNaCntOff + na_align((size_t)kNaRows * zi::kMaxGHost * 4);
+constexpr size_t kNaClsOff = kNaTicketOff + na_align((size_t)kNaRows * 4);
+constexpr size_t kNaRawOff = kNaClsOff + na_align((size_t)kNaRows * zi::kMaxGHost * 16 * 8);
+constexpr size_t kNaTop2Off = kNaRawOff + na_align((size_t)kNaRows * zi::kMaxGHost * 16 * 4);
+constexpr size_t kNaTailOff = kNaTop2Off + na_align((size_t)kNaRows * zi::kMaxGHost * 2 * 4);
+constexpr size_t kNaBytes = kNaTailOff + na_align((size_t)kNaRows * 16 * 4);
+static_assert(kNaBytes <= (size_t)8 << 20, "the static scratch stays under 8 MiB");
+
+std::mutex g_na_mu;
+constexpr int kNaMaxDevices = 64;
+uint8_t *g_na_ptr[kNaMaxDevices];  // device address of `scratch` on each device (hipGetSymbolAddress)
+}  // namespace
+
+// The scratch array itself.  In host code its name only stands for the
+// symbol; kernels get the per-device address from hipGetSymbolAddress.
+static __device__ __align__(256) uint8_t scratch[kNaBytes];
+
+// Zeroes the first n tickets (a kernel, not hipMemsetAsync, so that the call
+// can be captured into a HIP graph).
+__global__ void na_zero_tickets(int32_t *t, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) t[i] = 0;
+}
+
+static int32_t noalloc_scratch(int dev, Scratch &S) {
+    if (dev < 0 || dev >= kNaMaxDevices)
+        return zi_fail(ZI_ERR_UNSUPPORTED, "zi_sample_rows_noalloc: device %d >= %d", dev, kNaMaxDevices);
+    uint8_t *base;
+    {
+        std::lock_guard<std::mutex> lk(g_na_mu);
+        if (!g_na_ptr[dev]) {  // once per device, with that device current
+            void *ptr = nullptr;
+            hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+            if (e != hipSuccess) return zi_hip_fail(e, "zi_sample_rows_noalloc: hipGetSymbolAddress(scratch)");
+            if (!ptr) return zi_fail(ZI_ERR_HIP, "zi_sample_rows_noalloc: scratch has no device address");
+            g_na_ptr[dev] = (uint8_t *)ptr;
+        }
+        base = g_na_ptr[dev];
+    }
+    S.g_key = (uint64_t *)(base + kNaKeyOff);
+    S.g_val = (float *)(base + kNaValOff);
+    S.g_cnt = (int32_t *)(base + kNaCntOff);
+    S.tickets = (int32_t *)(base + kNaTicketOff);
+    S.g_cls = (uint64_t *)(base + kNaClsOff);
+    S.g_raw = (uint32_t *)(base + kNaRawOff);
+    S.g_top2 = (float *)(base + kNaTop2Off);
+    S.g_tail = (float *)(base + kNaTailOff);
+    S.win_ids = nullptr;  // no compaction buffer: hist_ld <= kMaxWinHost
+    S.win_len = nullptr;
+    return ZI_OK;
+}
+
+extern "C" int32_t zi_sample_rows_noalloc(const zi_params *p, const zi_batch *b, const float *uniforms,
+                                          const zi_sample_out *out, void *stream) {
+    const char *fn = "zi_sample_rows_noalloc";
+    // every size check before any HIP call
+    if (!p || !b || !out || !out->tok || !out->margin)
+        return zi_fail(ZI_ERR_INVALID, "%s: NULL params/batch/out/tok/margin", fn);
+    if (!b->logits) return zi_fail(ZI_ERR_INVALID, "%s: logits is NULL", fn);
+    if (b->dtype != ZI_F32 && b->dtype != ZI_BF16) return zi_fail(ZI_ERR_INVALID, "%s: dtype %d", fn, b->dtype);
+    if (b->rows < 1 || b->vocab < 1) return zi_fail(ZI_ERR_INVALID, "%s: rows=%d vocab=%d", fn, b->rows, b->vocab);
+    if (b->rows > kNaRows) return zi_fail(ZI_ERR_CAPACITY, "%s: rows=%d > %d", fn, b->rows, kNaRows);
+    if (b->vocab > zi::kMaxVocab) return zi_fail(ZI_ERR_CAPACITY, "%s: vocab=%d > %d", fn, b->vocab, zi::kMaxVocab);
+    if (b->ld < b->vocab || (b->ld % 8) != 0)
+        return zi_fail(ZI_ERR_INVALID, "%s: ld=%d must be >= vocab and a multiple of 8", fn, b->ld);
+    if (((uintptr_t)b->logits & 15u) != 0) return zi_fail(ZI_ERR_INVALID, "%s: logits not 16-byte aligned", fn);
+    if (p->temp > 0.0f) {
+        const uint32_t V = (uint32_t)b->vocab;
+        const uint32_t k = (p->top_k == 0 || p->top_k > V) ? V : p->top_k;
+        if (k > (uint32_t)zi::kMaxTopK)
+            return zi_fail(ZI_ERR_UNSUPPORTED, "%s: top_k resolves to %u > %d (whole-order sorting needs a context)",
+                           fn, k, zi::kMaxTopK);
+    }
+    if (b->hist && b->hist_ld > zi::kMaxWinHost)
+        return zi_fail(ZI_ERR_UNSUPPORTED, "%s: hist_ld=%d > %d", fn, b->hist_ld, zi::kMaxWinHost);
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev), "hipGetDevice");
+    Scratch S;
+    int32_t rc = noalloc_scratch(dev, S);
+    if (rc) return rc;
+    hipStream_t st = (hipStream_t)stream;
+    hipLaunchKernelGGL(na_zero_tickets, dim3((b->rows + 255) / 256), dim3(256), 0, st, S.tickets, b->rows);
+    HIP_TRY(hipGetLastError(), "zi_sample_rows_noalloc: ticket clear launch");
+    return sample_core(nullptr, S, st, p, b, uniforms, out, fn);
+}
