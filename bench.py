@@ -30,12 +30,13 @@ METRIC = "rows/sec + HBM GB/s (% of peak), 64×128256 f32 top-k/top-p sampling"
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2048)
-    ap.add_argument("--warmup", type=int, default=128)
+    ap.add_argument("--steps", type=int, default=2048, help="timed launches (exactly)")
+    ap.add_argument("--warmup", type=int, default=128, help="untimed launches before them (exactly)")
     ap.add_argument("--config", type=int, default=2, help="BASELINE config to run (2 = headline)")
-    ap.add_argument("--path", choices=["sample", "json_mask", "verify", "dry"], default="sample",
+    ap.add_argument("--path", choices=["sample", "json_mask", "verify", "dry", "readfloor"], default="sample",
                     help="sample: zi_sample_rows on --config (the headline); json_mask: zi_json_mask_rows; "
-                         "verify: zi_sampler_verify")
+                         "verify: zi_sampler_verify; dry: zi_dry_edits_rows; readfloor: a plain read of "
+                         "config 2's bytes (the achievable-bandwidth reference)")
     ap.add_argument("--branches", type=int, default=1,
                     help="verify path: > 1 verifies that many 8-token branches in one call (zi_sampler_verify_tree)")
     ap.add_argument("--softcap", type=float, default=0.0,
@@ -85,6 +86,116 @@ def read_traffic(path: str, kernel: str, workload: str):
         if m and m.group(1) == workload and m.group(2) == kernel:
             return float(m.group(3))
     return None
+
+
+def timed_launches(launch, nsets: int, steps: int, warmup: int, stream, use_graph: bool = True):
+    """Runs exactly `warmup` untimed then `steps` timed launches, launch i
+    working on input set i % nsets, on `stream` (the caller has made it
+    current).  With graphs: one graph of all nsets launches, replayed
+    steps // nsets times, plus a graph of the first steps % nsets launches
+    (likewise for the warmup).  Returns (gpu ms over the timed launches from
+    HIP events on `stream`, host wall seconds)."""
+    import torch
+
+    graphs = {}
+
+    def graph_of(n):
+        if n not in graphs:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                for i in range(n):
+                    launch(i)
+            torch.cuda.synchronize()
+            graphs[n] = g
+        return graphs[n]
+
+    def run(n):
+        if not use_graph:
+            for i in range(n):
+                launch(i % nsets)
+            return
+        full, rem = divmod(n, nsets)
+        for _ in range(full):
+            graph_of(nsets).replay()
+        if rem:
+            graph_of(rem).replay()
+
+    for i in range(nsets):  # eager first pass: any lazy set-up happens outside the graphs
+        launch(i)
+    torch.cuda.synchronize()
+    if use_graph:  # capture before timing
+        graph_of(nsets)
+        if steps % nsets:
+            graph_of(steps % nsets)
+        if warmup % nsets:
+            graph_of(warmup % nsets)
+    run(warmup)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    run(steps)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    return ev0.elapsed_time(ev1), time.perf_counter() - t0
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def host_threads() -> int:
+    """Worker threads for the all-cores CPU leg: the box's CPU share (its
+    OMP_NUM_THREADS), else the visible cores."""
+    n = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    return max(1, n or (os.cpu_count() or 1))
+
+
+def bench_readfloor(args):
+    """A plain streaming read of config 2's bytes (zi_probe.hip, 1024-thread
+    workgroups, 128 KiB each, non-temporal 16-byte loads) in the same harness
+    as the sampling path: rotating input sets, graph replay, HIP events.  It
+    is the achievable-bandwidth reference for the sampling kernels (and its
+    per-launch time includes the same launch overhead)."""
+    import ctypes as C
+
+    import torch
+
+    lib = C.CDLL(os.path.join(ROOT, "zinfer_amd", "libzi_probe.so"))
+    lib.zi_probe_read.restype = C.c_int32
+    lib.zi_probe_read.argtypes = [C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p]
+    dev = torch.device("cuda:0")
+    nbytes = 64 * 128256 * 4
+    nsets = max(1, (args.rotate_mib * 2**20 + nbytes - 1) // nbytes)
+    sets = [torch.empty(nbytes // 4, dtype=torch.float32, device=dev).uniform_() for _ in range(nsets)]
+    out = torch.empty(((nbytes + 131071) // 131072) * 16, dtype=torch.float32, device=dev)
+    stream = torch.cuda.Stream(dev)
+
+    def launch(i):
+        rc = lib.zi_probe_read(sets[i].data_ptr(), nbytes, out.data_ptr(), stream.cuda_stream)
+        assert rc == 0, rc
+
+    with torch.cuda.stream(stream):
+        gpu_ms, wall = timed_launches(launch, nsets, args.steps, args.warmup, stream, not args.no_graph)
+    ms = gpu_ms / args.steps
+    achieved = nbytes / (ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "plain streaming read of 64x128256 f32 (achievable-bandwidth reference)",
+        "value": round(achieved, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (torch uniform_)",
+        "config": {"workload": "readfloor_64x128256_f32", "bytes": nbytes, "rotating_input_sets": nsets,
+                   "launch": "eager" if args.no_graph else "hip_graph_replay"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": nbytes, "kernel": "read_kernel"},
+        "cpu_baseline": None, "wall_s": round(wall, 3)}), flush=True)
 
 
 def bench_json_mask(args):
@@ -404,29 +515,11 @@ def bench_entropy(args, w):
     draft = torch.from_numpy(w.draft.astype(np.int32)).to(dev)
     ctx = Context(0, max_rows=rows, max_vocab=V)
     stream = torch.cuda.Stream(dev)
+    steps = args.steps
     with torch.cuda.stream(stream):
-        for i in range(nsets):
-            ctx.entropy_topk_rows(sets[i], k, draft)
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=stream):
-            for i in range(nsets):
-                ctx.entropy_topk_rows(sets[i], k, draft)
-        torch.cuda.synchronize()
-        reps = max(1, args.steps // nsets)
-        for _ in range(max(1, args.warmup // nsets)):
-            graph.replay()
-        torch.cuda.synchronize()
-        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        t0 = time.perf_counter()
-        ev0.record(stream)
-        for _ in range(reps):
-            graph.replay()
-        ev1.record(stream)
-        torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-    steps = reps * nsets
-    ms = ev0.elapsed_time(ev1) / steps
+        gpu_ms, wall = timed_launches(lambda i: ctx.entropy_topk_rows(sets[i], k, draft), nsets, steps, args.warmup,
+                                      stream, not args.no_graph)
+    ms = gpu_ms / steps
     ent, ids, probs, am, acc = ctx.entropy_topk_rows(sets[0], k, draft)
     torch.cuda.synchronize()
     cpu = None
@@ -451,7 +544,7 @@ def bench_entropy(args, w):
     print(json.dumps({
         "metric": "rows/sec + HBM GB/s (% of peak), 64x262144 f32 entropy + top-8 + accept",
         "value": round(rows / (ms * 1e-3), 1), "unit": "rows/s", "n_gpus": 1, "steps": steps,
-        "warmup": max(1, args.warmup // nsets) * nsets, "ms_per_step": round(ms, 6), "higher_is_better": True,
+        "warmup": args.warmup, "ms_per_step": round(ms, 6), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic, seeded (zinfer_amd/workloads.py): " + w.name,
         "config": {"workload": w.name, "rows": rows, "vocab": V, "k": k, "rotating_input_sets": nsets,
@@ -488,6 +581,9 @@ def main():
         return
     if args.path == "dry":
         bench_dry(args)
+        return
+    if args.path == "readfloor":
+        bench_readfloor(args)
         return
 
     import numpy as np
@@ -543,40 +639,9 @@ def main():
                         groups=gdev, group_count=cdev)
 
     stream = torch.cuda.Stream(dev)  # default priority
+    steps, wsteps = args.steps, args.warmup
     with torch.cuda.stream(stream):
-        for i in range(nsets):
-            launch(i)
-        torch.cuda.synchronize()
-        graph = None
-        if not args.no_graph:
-            graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph, stream=stream):
-                for i in range(nsets):
-                    launch(i)
-            torch.cuda.synchronize()
-        reps = max(1, args.steps // nsets)
-        steps = reps * nsets
-        wreps = max(1, args.warmup // nsets)
-
-        def run(nrep):
-            for _ in range(nrep):
-                if graph is not None:
-                    graph.replay()
-                else:
-                    for i in range(nsets):
-                        launch(i)
-
-        run(wreps)
-        torch.cuda.synchronize()
-        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        ev0.record(stream)
-        run(reps)
-        ev1.record(stream)
-        torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-        gpu_ms = ev0.elapsed_time(ev1)
+        gpu_ms, wall = timed_launches(launch, nsets, steps, wsteps, stream, not args.no_graph)
 
     ms_per_step = gpu_ms / steps
     rows_per_s = rows / (ms_per_step * 1e-3)
@@ -632,6 +697,32 @@ def main():
                # the north star's count of chosen-token disagreements (top-p boundary or other) on the
                # rows both sides sampled; the kernels are bit-exact, so any nonzero count is a bug
                "id_mismatches": int(np.count_nonzero(gtok != tokc)), "rows_compared": int(n_rows_cpu)}
+        # the same sample with rows spread over the host's cores (the reference sampler is
+        # single-threaded; this is the planned second leg): one thread per core, each passing
+        # over its own slice of the rows; ctypes releases the GIL during the oracle call
+        from concurrent.futures import ThreadPoolExecutor
+
+        nth = min(host_threads(), n_rows_cpu)
+        bounds = np.linspace(0, n_rows_cpu, nth + 1).astype(int)
+        creps_all = max(1, creps * nth // 2)  # about half the 1-core leg's time at full scaling
+
+        def part(i):
+            a, b = bounds[i], bounds[i + 1]
+            return pyoracle.bench_sample_rows(op, np.ascontiguousarray(L[a:b]),
+                                              w.hist[a:b] if w.hist is not None else None,
+                                              w.hist_len[a:b] if w.hist is not None else None,
+                                              w.mask[a:b] if w.mask is not None else None, w.uniforms[a:b],
+                                              creps_all)
+
+        with ThreadPoolExecutor(nth) as ex:
+            tw0 = time.perf_counter()
+            res = list(ex.map(part, range(nth)))
+            tw = time.perf_counter() - tw0
+        tok_all = np.concatenate([r[1] for r in res]).astype(np.uint32)
+        cpu["all_cores"] = {"value": round(n_rows_cpu * creps_all / tw, 1), "unit": "rows/s", "cores": nth,
+                            "cpu_model": cpu_model(),
+                            "sample": f"{n_rows_cpu} rows x {creps_all} passes over {nth} threads ({tw:.1f} s)",
+                            "tokens_match_gpu": bool(np.array_equal(gtok, tok_all))}
 
     out = {
         "metric": METRIC,
@@ -639,7 +730,7 @@ def main():
         "unit": "rows/s",
         "n_gpus": 1,
         "steps": steps,
-        "warmup": wreps * nsets,
+        "warmup": wsteps,
         "ms_per_step": round(ms_per_step, 6),
         "higher_is_better": True,
         "scaling": "weak",

@@ -95,6 +95,19 @@ void    zi_destroy(zi_ctx *ctx);
  * (null) stream. */
 int32_t zi_set_stream(zi_ctx *ctx, void *stream);
 int32_t zi_sync(zi_ctx *ctx);
+
+/* Allocates now the scratch that some requests otherwise allocate on their
+ * first call, so that no later call on the context allocates (code under HIP
+ * graph capture, serving loops).  No reference counterpart.  Synchronous.
+ *   ZI_RESERVE_WHOLE_ORDER   top_k = 0 or > 256 (whole-order sorting):
+ *                            20 B x max_rows x max_vocab (rounded up to 8)
+ *                            + 4 B x max_rows
+ *   ZI_RESERVE_PRUNED_DENSE  zi_sample_rows_pruned with a softcap or top_k >
+ *                            256 (the reference's filled rows):
+ *                            4 B x max_rows x max_vocab (rounded up to 8) */
+#define ZI_RESERVE_WHOLE_ORDER 1u
+#define ZI_RESERVE_PRUNED_DENSE 2u
+int32_t zi_reserve(zi_ctx *ctx, uint32_t what);
 const char *zi_last_error(void);
 int32_t zi_abi_version(void);
 
@@ -147,8 +160,8 @@ typedef struct zi_sample_out {
  * the rows it cannot settle; 256 < top_k < V always sorts.  For top_k > 256
  * (with V > 256) cand_ids/cand_vals/probs hold the first min(keep, cand_ld)
  * candidates (cand_ld >= 1), and the first such call allocates 20 bytes of
- * sort scratch per (max_rows x max_vocab) entry.  Penalty window + edits <=
- * 1024 + 128 ids. */
+ * sort scratch per (max_rows x max_vocab) entry unless zi_reserve did.
+ * Penalty window + edits <= 1024 + 128 ids. */
 int32_t zi_sample_rows(zi_ctx *ctx, const zi_params *p, const zi_batch *b,
                        const float *uniforms, const zi_sample_out *out);
 
@@ -180,8 +193,8 @@ int32_t zi_sample_rows_noalloc(const zi_params *p, const zi_batch *b, const floa
  * once.  Results are those of zi_sample_rows on the row with the fill
  * written.  With final_logit_softcap (which runs after the fill and moves it
  * to -cap*tanh(9)) or top_k resolving to > 256 (lists that order every id),
- * the filled rows are written to a context scratch, allocated on first use,
- * and sampled by zi_sample_rows.  Limits: groups_ld <= 1024 (the reference
+ * the filled rows are written to a context scratch (zi_reserve, else
+ * allocated on first use) and sampled by zi_sample_rows.  Limits: groups_ld <= 1024 (the reference
  * keeps 576), V >= 16; each returns ZI_ERR_UNSUPPORTED. */
 int32_t zi_sample_rows_pruned(zi_ctx *ctx, const zi_params *p, const zi_batch *b,
                               const uint32_t *groups, const int32_t *group_count,

@@ -321,9 +321,11 @@ static void stable_sort_desc(cand_t *a, uint32_t n) {
     free(tmp);
 }
 
-static cand_t *g_cand = NULL; /* Sampler.cand, src/sampler.zig:41, :53 */
-static uint32_t g_cand_cap = 0;
-static float *g_w = NULL;
+/* Sampler.cand (src/sampler.zig:41, :53), one per calling thread so that the
+ * CPU baseline can run rows on several threads at once. */
+static _Thread_local cand_t *g_cand = NULL;
+static _Thread_local uint32_t g_cand_cap = 0;
+static _Thread_local float *g_w = NULL;
 
 static void ensure_cand(uint32_t V) {
     if (V > g_cand_cap) {

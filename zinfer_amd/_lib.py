@@ -20,6 +20,8 @@ ZI_ERR_UNSUPPORTED = -4
 ZI_ERR_CAPACITY = -5
 ZI_F32 = 0
 ZI_BF16 = 1
+ZI_RESERVE_WHOLE_ORDER = 1
+ZI_RESERVE_PRUNED_DENSE = 2
 
 u32p = C.POINTER(C.c_uint32)
 f32p = C.POINTER(C.c_float)
@@ -117,6 +119,7 @@ SIGNATURES = {
     "zi_destroy": (None, [C.c_void_p]),
     "zi_set_stream": (C.c_int32, [C.c_void_p, C.c_void_p]),
     "zi_sync": (C.c_int32, [C.c_void_p]),
+    "zi_reserve": (C.c_int32, [C.c_void_p, C.c_uint32]),
     "zi_last_error": (C.c_char_p, []),
     "zi_sample_rows_noalloc": (C.c_int32, [C.POINTER(ZiParams), C.POINTER(ZiBatch), C.c_void_p,
                                            C.POINTER(ZiSampleOut), C.c_void_p]),

@@ -63,6 +63,10 @@ class Context:
         except Exception:
             pass
 
+    def reserve(self, what: int):
+        """zi_reserve: allocate the lazily allocated scratch now (ZI_RESERVE_* bits)."""
+        check(lib().zi_reserve(self.h, what))
+
     def _bind_stream(self):
         s = torch.cuda.current_stream(self.device)
         check(lib().zi_set_stream(self.h, C.c_void_p(s.cuda_stream)))

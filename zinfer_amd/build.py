@@ -15,6 +15,10 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libzinfer_hip.so")
+PROBE_LIB = os.path.join(PKG, "libzi_probe.so")  # bench.py's plain-read reference, not the sampling ABI
+# tests/test_gpu_capi.py's C caller of the ABI (gcc, header + shared library only)
+CONSUMER_SRC = os.path.join(ROOT, "tests", "capi", "consumer.c")
+CONSUMER = os.path.join(ROOT, "tests", "capi", "zi_consumer")
 OBJ = os.path.join(ROOT, "_build", "obj")
 
 SOURCES = ["zi_sample.hip", "zi_sample_cap.hip", "zi_exact.hip", "zi_argmax.hip", "zi_entropy.hip", "zi_grammar.hip", "zi_pruned.hip", "zi_dry.hip",
@@ -48,8 +52,20 @@ def build(verbose: bool = False) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
     os.replace(tmp, LIB)
+    probe_obj = _compile("zi_probe.hip")
+    tmp = PROBE_LIB + ".tmp"
+    r = subprocess.run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", probe_obj, "-o", tmp],
+                       capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed (probe):\n{r.stderr}")
+    os.replace(tmp, PROBE_LIB)
+    r = subprocess.run(["gcc", "-O2", "-std=c11", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"), CONSUMER_SRC,
+                        "-L", PKG, "-lzinfer_hip", "-Wl,-rpath,$ORIGIN/../../zinfer_amd", "-o", CONSUMER],
+                       capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"gcc failed for the C consumer:\n{r.stderr}")
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB}, {PROBE_LIB} and {CONSUMER}")
     return LIB
 
 

@@ -118,16 +118,26 @@ extern "C" int32_t zi_create(zi_ctx **out, int32_t device, int32_t max_rows, int
     return ZI_OK;
 }
 
+// zi_destroy cannot report; the first failing HIP call is left in
+// zi_last_error() and the rest of the teardown still runs.
 extern "C" void zi_destroy(zi_ctx *c) {
     if (!c) return;
-    hipSetDevice(c->device);
-    if (c->own_stream) hipStreamSynchronize(c->own_stream);
+    hipError_t first = hipSuccess;
+    const char *what = nullptr;
+    auto note = [&](hipError_t e, const char *w) {
+        if (e != hipSuccess && first == hipSuccess) {
+            first = e;
+            what = w;
+        }
+    };
+    note(hipSetDevice(c->device), "zi_destroy: hipSetDevice");
+    if (c->own_stream) note(hipStreamSynchronize(c->own_stream), "zi_destroy: hipStreamSynchronize");
     void *ptrs[] = {c->g_key,  c->g_val,   c->g_cnt,   c->tickets, c->g_stat,  c->g_cls,   c->g_raw,
-                    c->g_top2, c->g_tail,  c->win_ids, c->win_len, c->ex_sort, c->nuc_flag};
+                    c->g_top2, c->g_tail,  c->win_ids, c->win_len, c->ex_sort, c->nuc_flag, c->pr_dense};
     for (void *p : ptrs)
-        if (p) hipFree(p);
-    if (c->pr_dense) hipFree(c->pr_dense);
-    if (c->own_stream) hipStreamDestroy(c->own_stream);
+        if (p) note(hipFree(p), "zi_destroy: hipFree");
+    if (c->own_stream) note(hipStreamDestroy(c->own_stream), "zi_destroy: hipStreamDestroy");
+    if (first != hipSuccess) zi_hip_fail(first, what);
     delete c;
 }
 
@@ -274,27 +284,75 @@ static int32_t run_argmax(const Scratch &S, hipStream_t st, const zi::RowSource 
     return ZI_OK;
 }
 
+// The whole-order sort scratch: 5 planes of [max_rows][max_vocab rounded up
+// to 8] u32 and the per-row settle flags.  Allocated by zi_reserve, or by the
+// first request that needs it.
+static int32_t ensure_whole_order(zi_ctx *c) {
+    if (c->ex_sort) return ZI_OK;
+    const int64_t ld = ((int64_t)c->max_vocab + 7) / 8 * 8;
+    const size_t bytes = 5 * (size_t)c->max_rows * (size_t)ld * sizeof(uint32_t);
+    hipError_t e = hipMalloc((void **)&c->ex_sort, bytes);
+    if (e == hipSuccess) e = hipMalloc((void **)&c->nuc_flag, (size_t)c->max_rows * sizeof(int32_t));
+    if (e != hipSuccess) {
+        if (c->ex_sort) {
+            const hipError_t ef = hipFree(c->ex_sort);
+            if (ef != hipSuccess) e = ef;
+        }
+        c->ex_sort = nullptr;
+        c->nuc_flag = nullptr;
+        return zi_fail(ZI_ERR_OOM, "sort scratch %zu bytes: %s", bytes, hipGetErrorString(e));
+    }
+    c->ex_ld = ld;
+    return ZI_OK;
+}
+
+// Dense rows for zi_sample_rows_pruned's dense path, at least `need` bytes
+// (zi_reserve takes max_rows x max_vocab rounded up to 8 x 4 bytes, enough
+// for every batch).
+static int32_t ensure_pruned_dense(zi_ctx *c, size_t need) {
+    if (need <= c->pr_dense_bytes) return ZI_OK;
+    if (c->pr_dense) {
+        const hipError_t ef = hipFree(c->pr_dense);
+        c->pr_dense = nullptr;
+        c->pr_dense_bytes = 0;
+        if (ef != hipSuccess) return zi_hip_fail(ef, "pruned dense scratch release");
+    }
+    const hipError_t e = hipMalloc(&c->pr_dense, need);
+    if (e != hipSuccess) {
+        c->pr_dense = nullptr;
+        return zi_fail(ZI_ERR_OOM, "pruned dense scratch %zu bytes: %s", need, hipGetErrorString(e));
+    }
+    c->pr_dense_bytes = need;
+    return ZI_OK;
+}
+
+extern "C" int32_t zi_reserve(zi_ctx *c, uint32_t what) {
+    if (!c) return zi_fail(ZI_ERR_INVALID, "zi_reserve: ctx is NULL");
+    if (what & ~(uint32_t)(ZI_RESERVE_WHOLE_ORDER | ZI_RESERVE_PRUNED_DENSE))
+        return zi_fail(ZI_ERR_INVALID, "zi_reserve: unknown flags 0x%x", what);
+    HIP_TRY(hipSetDevice(c->device), "zi_reserve: hipSetDevice");
+    if (what & ZI_RESERVE_WHOLE_ORDER) {
+        const int32_t rc = ensure_whole_order(c);
+        if (rc) return rc;
+    }
+    if (what & ZI_RESERVE_PRUNED_DENSE) {
+        const size_t ld = ((size_t)c->max_vocab + 7) / 8 * 8;
+        const int32_t rc = ensure_pruned_dense(c, (size_t)c->max_rows * ld * sizeof(float));
+        if (rc) return rc;
+    }
+    return ZI_OK;
+}
+
 // Candidate lists longer than kMaxTopK.  k = V: nucleus_kernel settles the
 // rows whose keep its 256-entry prefix fixes and flags the rest for
 // exact_kernel; 256 < k < V: exact_kernel on every row.  The sort scratch
-// (20 bytes per row entry) is allocated on first use.
+// (20 bytes per row entry) comes from ensure_whole_order.
 static int32_t run_whole_order(zi_ctx *c, const zi_params *p, const zi_batch *b, const zi::RowSource &src,
                                const zi::Plan &pl, uint32_t k, const float *uniforms, const zi_sample_out *out) {
     if ((out->cand_ids || out->cand_vals || out->probs) && out->cand_ld < 1)
         return zi_fail(ZI_ERR_INVALID, "zi_sample_rows: cand_ld=%d < 1", out->cand_ld);
-    if (!c->ex_sort) {
-        const int64_t ld = ((int64_t)c->max_vocab + 7) / 8 * 8;
-        const size_t bytes = 5 * (size_t)c->max_rows * (size_t)ld * sizeof(uint32_t);
-        hipError_t e = hipMalloc((void **)&c->ex_sort, bytes);
-        if (e == hipSuccess) e = hipMalloc((void **)&c->nuc_flag, (size_t)c->max_rows * sizeof(int32_t));
-        if (e != hipSuccess) {
-            if (c->ex_sort) hipFree(c->ex_sort);
-            c->ex_sort = nullptr;
-            c->nuc_flag = nullptr;
-            return zi_fail(ZI_ERR_OOM, "zi_sample_rows: sort scratch %zu bytes: %s", bytes, hipGetErrorString(e));
-        }
-        c->ex_ld = ld;
-    }
+    const int32_t rc = ensure_whole_order(c);
+    if (rc) return rc;
     const uint32_t V = (uint32_t)b->vocab;
     const bool whole = k >= V;
     if (whole) {
@@ -453,20 +511,15 @@ extern "C" int32_t zi_sample_rows_pruned(zi_ctx *c, const zi_params *p, const zi
         // id.  Both take the dense path on the row the reference builds.
         if (p->final_logit_softcap > 0.0f || (p->temp > 0.0f && k0 > (uint32_t)zi::kMaxTopK)) {
             const size_t elt = b->dtype == ZI_F32 ? 4 : 2;
-            const size_t need = (size_t)b->rows * (size_t)b->ld * elt;
-            if (need > c->pr_dense_bytes) {
-                if (c->pr_dense) hipFree(c->pr_dense);
-                c->pr_dense = nullptr;
-                c->pr_dense_bytes = 0;
-                hipError_t e = hipMalloc(&c->pr_dense, need);
-                if (e != hipSuccess) return zi_hip_fail(e, "zi_sample_rows_pruned: dense scratch");
-                c->pr_dense_bytes = need;
-            }
-            hipError_t e = zi::launch_pruned_fill(b->logits, c->pr_dense, b->ld, b->vocab, b->rows, b->dtype, groups,
-                                                  group_count, groups_ld, c->stream);
+            const int64_t dld = ((int64_t)b->vocab + 7) / 8 * 8;  // the dense rows' own stride
+            rc = ensure_pruned_dense(c, (size_t)b->rows * (size_t)dld * elt);
+            if (rc) return rc;
+            hipError_t e = zi::launch_pruned_fill(b->logits, c->pr_dense, b->ld, dld, b->vocab, b->rows, b->dtype,
+                                                  groups, group_count, groups_ld, c->stream);
             if (e != hipSuccess) return zi_hip_fail(e, "pruned fill launch");
             zi_batch bd = *b;
             bd.logits = c->pr_dense;
+            bd.ld = (int32_t)dld;
             return zi_sample_rows(c, p, &bd, uniforms, out);
         }
     }

@@ -246,19 +246,19 @@ bool zi_vocab_piece(const zi_vocab *v, uint32_t id, const uint8_t **p, uint32_t 
     return true;
 }
 
+// Frees every buffer; the first failure is left in zi_last_error() (the
+// callers cannot report it) and the rest still runs.
 static void release(zi_vocab *v) {
     if (!v) return;
-    hipFree(v->rec);
-    hipFree(v->tails);
-    hipFree(v->toff);
-    hipFree(v->one);
-    hipFree(v->tables);
-    hipFree(v->base);
-    hipFree(v->list);
-    hipFree(v->lrec);
-    hipFree(v->ltails);
-    hipFree(v->ltoff);
-    hipFree(v->cache);
+    void *bufs[] = {v->rec, v->tails, v->toff, v->one, v->tables, v->base, v->list, v->lrec, v->ltails, v->ltoff,
+                    v->cache};
+    hipError_t first = hipSuccess;
+    for (void *p : bufs) {
+        if (!p) continue;
+        const hipError_t e = hipFree(p);
+        if (e != hipSuccess && first == hipSuccess) first = e;
+    }
+    if (first != hipSuccess) zi_hip_fail(first, "zi_vocab release: hipFree");
     delete v;
 }
 

@@ -102,17 +102,31 @@ struct Staging {
     void *h = nullptr;  // pinned host
     void *d = nullptr;  // device
     size_t bytes = 0;
+    // Frees both buffers; returns the first failure (hipSuccess if none).
+    hipError_t release() {
+        hipError_t e = hipSuccess;
+        if (h) {
+            const hipError_t eh = hipHostFree(h);
+            if (eh != hipSuccess) e = eh;
+        }
+        if (d) {
+            const hipError_t ed = hipFree(d);
+            if (ed != hipSuccess && e == hipSuccess) e = ed;
+        }
+        h = d = nullptr;
+        bytes = 0;
+        return e;
+    }
     ~Staging() {
-        if (h) hipHostFree(h);
-        if (d) hipFree(d);
+        // a destructor cannot report: a failure is left in zi_last_error()
+        const hipError_t e = release();
+        if (e != hipSuccess) zi_hip_fail(e, "staging release");
     }
     int32_t ensure(size_t n) {
         if (n <= bytes) return ZI_OK;
-        if (h) hipHostFree(h);
-        if (d) hipFree(d);
-        h = d = nullptr;
-        bytes = 0;
-        hipError_t e = hipHostMalloc(&h, n, hipHostMallocDefault);
+        hipError_t e = release();
+        if (e != hipSuccess) return zi_hip_fail(e, "staging release");
+        e = hipHostMalloc(&h, n, hipHostMallocDefault);
         if (e == hipSuccess) e = hipMalloc(&d, n);
         if (e != hipSuccess) return zi_fail(ZI_ERR_OOM, "staging allocation of %zu bytes: %s", n, hipGetErrorString(e));
         bytes = n;
@@ -237,7 +251,11 @@ extern "C" int32_t zi_sampler_init(zi_sampler **out, zi_ctx *ctx, uint32_t vocab
     s->o_ndraws = o;
     o += 16;
     s->total = align_up(o, 256);
-    hipSetDevice(ctx->device);
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e != hipSuccess) {
+        delete s;
+        return zi_hip_fail(e, "zi_sampler_init: hipSetDevice");
+    }
     int32_t rc = s->st.ensure(s->total);
     if (rc) {
         delete s;
@@ -322,8 +340,9 @@ extern "C" int32_t zi_sampler_sample_with_margin(zi_sampler *s, float *logits, u
     u[1] = peek.f32();
     *(int32_t *)(h + s->o_ndraws) = 0;  // not every path writes ndraws
 
-    hipSetDevice(c->device);
-    hipError_t e = hipMemcpyAsync(d, h, s->o_ndraws + 16, hipMemcpyHostToDevice, c->stream);
+    hipError_t e = hipSetDevice(c->device);
+    if (e != hipSuccess) return zi_hip_fail(e, "sampler: hipSetDevice");
+    e = hipMemcpyAsync(d, h, s->o_ndraws + 16, hipMemcpyHostToDevice, c->stream);
     if (e != hipSuccess) return zi_hip_fail(e, "sampler H2D");
     zi_batch b;
     std::memset(&b, 0, sizeof b);
@@ -604,11 +623,12 @@ extern "C" int32_t zi_argmax_with_margin(zi_ctx *c, const float *logits, uint32_
     static thread_local Staging st;
     const uint32_t ld = (n + 7u) & ~7u;
     const size_t o_out = align_up((size_t)ld * 4, 256);
-    hipSetDevice(c->device);
+    hipError_t e = hipSetDevice(c->device);
+    if (e != hipSuccess) return zi_hip_fail(e, "zi_argmax_with_margin: hipSetDevice");
     int32_t rc = st.ensure(o_out + 256);
     if (rc) return rc;
     std::memcpy(st.h, logits, (size_t)n * 4);
-    hipError_t e = hipMemcpyAsync(st.d, st.h, (size_t)n * 4, hipMemcpyHostToDevice, c->stream);
+    e = hipMemcpyAsync(st.d, st.h, (size_t)n * 4, hipMemcpyHostToDevice, c->stream);
     if (e != hipSuccess) return zi_hip_fail(e, "argmax H2D");
     zi_batch b;
     std::memset(&b, 0, sizeof b);

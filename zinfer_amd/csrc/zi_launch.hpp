@@ -138,8 +138,8 @@ hipError_t launch_sample(const SampleParams &P, int dtype, int nv, int rows, hip
 hipError_t launch_nucleus(const SampleParams &P, int dtype, int nv, int rows, hipStream_t st);
 hipError_t launch_pruned(const SampleParams &P, int dtype, int rows, hipStream_t st);
 // Writes the row the reference's pruned lm_head leaves (-inf, then the listed
-// groups' logits) into dense [rows][ld] for the dense sampling path.
-hipError_t launch_pruned_fill(const void *logits, void *dense, int64_t ld, int V, int rows, int dtype,
+// groups' logits) into dense [rows][dst_ld] for the dense sampling path.
+hipError_t launch_pruned_fill(const void *logits, void *dense, int64_t ld, int64_t dst_ld, int V, int rows, int dtype,
                               const uint32_t *groups, const int32_t *group_count, int groups_ld, hipStream_t st);
 // the final-logit softcap instances of launch_sample / launch_nucleus (zi_sample_cap.hip)
 hipError_t launch_sample_capped(const SampleParams &P, int dtype, int nv, int rows, hipStream_t st);

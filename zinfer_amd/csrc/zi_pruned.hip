@@ -407,7 +407,7 @@ __global__ __launch_bounds__(kThreads) void pruned_kernel(SampleParams P) {
 // group of 8: copied when listed, -inf otherwise (src/model.zig:2127-2128 then
 // :1156-1158).
 template <typename T>
-__global__ __launch_bounds__(kThreads) void pruned_fill_kernel(const T *src, T *dst, int64_t ld, int V,
+__global__ __launch_bounds__(kThreads) void pruned_fill_kernel(const T *src, T *dst, int64_t ld, int64_t dst_ld, int V,
                                                                const uint32_t *groups, const int32_t *group_count,
                                                                int groups_ld) {
     constexpr int VEC = VecTraits<T>::VEC;
@@ -429,7 +429,7 @@ __global__ __launch_bounds__(kThreads) void pruned_fill_kernel(const T *src, T *
     if (g >= ngt) return;
     const bool listed = (bits[tid >> 5] >> (tid & 31)) & 1u;
     const T *s = src + (int64_t)row * ld + g * 8u;
-    T *d = dst + (int64_t)row * ld + g * 8u;
+    T *d = dst + (int64_t)row * dst_ld + g * 8u;
     const uint32_t ninf = sizeof(T) == 4 ? 0xFF800000u : 0xFF80FF80u;  // -inf, as f32 or two bf16
 #pragma unroll
     for (int q = 0; q < NL; ++q) {
@@ -438,16 +438,16 @@ __global__ __launch_bounds__(kThreads) void pruned_fill_kernel(const T *src, T *
     }
 }
 
-hipError_t launch_pruned_fill(const void *logits, void *dense, int64_t ld, int V, int rows, int dtype,
+hipError_t launch_pruned_fill(const void *logits, void *dense, int64_t ld, int64_t dst_ld, int V, int rows, int dtype,
                               const uint32_t *groups, const int32_t *group_count, int groups_ld, hipStream_t st) {
     const int ngt = (V + 7) / 8;
     dim3 grid((ngt + kThreads - 1) / kThreads, rows), block(kThreads);
     if (dtype == 0)
         hipLaunchKernelGGL(pruned_fill_kernel<float>, grid, block, 0, st, static_cast<const float *>(logits),
-                           static_cast<float *>(dense), ld, V, groups, group_count, groups_ld);
+                           static_cast<float *>(dense), ld, dst_ld, V, groups, group_count, groups_ld);
     else
         hipLaunchKernelGGL(pruned_fill_kernel<uint16_t>, grid, block, 0, st, static_cast<const uint16_t *>(logits),
-                           static_cast<uint16_t *>(dense), ld, V, groups, group_count, groups_ld);
+                           static_cast<uint16_t *>(dense), ld, dst_ld, V, groups, group_count, groups_ld);
     return hipGetLastError();
 }
 
