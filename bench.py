@@ -41,6 +41,8 @@ def parse():
                     help="verify path: > 1 verifies that many 8-token branches in one call (zi_sampler_verify_tree)")
     ap.add_argument("--softcap", type=float, default=0.0,
                     help="final-logit softcap fused into the read (sample path; 0 = off, the config's default)")
+    ap.add_argument("--min-p", type=float, default=None,
+                    help="override the config's min_p (config 5 with 0 is the whole-order nucleus case)")
     ap.add_argument("--pruned", type=int, default=0,
                     help="pruned rows (sample path): 64 fixed + this many random groups of 8 ids per row are the "
                          "only logits (zi_sample_rows_pruned; the reference keeps 512); 0 = dense rows")
@@ -598,6 +600,9 @@ def main():
     rows, V = w.rows, w.vocab
     if args.softcap > 0:
         w.params = dict(w.params, final_logit_softcap=args.softcap)
+    if args.min_p is not None:
+        w.params = dict(w.params, min_p=args.min_p)
+        w.name += f"_minp{args.min_p:g}"
     if args.config == 4:
         bench_entropy(args, w)
         return
@@ -655,11 +660,11 @@ def main():
     top_k = w.params.get("top_k", 40)
     k_eff = V if (top_k == 0 or top_k > V) else top_k
     # the launch's dominant kernel: batches of >= 256 rows (kRowLoopRows in zi_sample.hip) run one
-    # workgroup per row
+    # workgroup per row; a whole-vocabulary nucleus with min_p > 0 runs the min-p prefix kernel there
     if gdev is not None:
         kernel = "pruned_kernel"
     elif rows >= 256:
-        kernel = "row_kernel"
+        kernel = "prefix_kernel" if (k_eff > 256 and w.params.get("min_p", 0.05) > 0) else "row_kernel"
     else:
         kernel = "nucleus_kernel" if k_eff > 256 else "sample_kernel"
     traffic = read_traffic(args.traffic, kernel, w.name)

@@ -148,6 +148,22 @@ def test_config5_full_size_parity(ctx, oracle):
     assert not errs, "\n".join(errs[:20])
 
 
+def test_config5_min_p_zero_full_size(ctx, oracle):
+    """Config 5 as its text names it, the worst-case nucleus: min_p = 0, so
+    top_p = 0.98 alone cuts the whole-vocabulary order (thousands of entries
+    per row) and every row takes the exact whole-order pass.  512 x 151936
+    bf16, bit-exact."""
+    from zinfer_amd.workloads import CONFIGS
+
+    w = CONFIGS[5]()
+    pk = dict(w.params, min_p=0.0)
+    g = gpu_sample(ctx, pk, w.logits, w.uniforms, w.hist, w.hist_len, bf16=True)
+    o = oracle_sample(oracle, pk, w.logits, w.uniforms, w.hist, w.hist_len)
+    errs = compare_sample(g, o, pk, w.vocab, w.name + "_minp0")
+    assert not errs, "\n".join(errs[:20])
+    assert int(np.median([d["keep"] for _, _, d in o])) > 1000  # the nucleus is long
+
+
 @pytest.mark.parametrize("min_p,top_p", [(0.05, 0.98), (0.3, 0.9), (0.0, 0.98)])
 def test_whole_vocab_large_batch(ctx, oracle, min_p, top_p):
     """>= 256 rows: the prefix pass runs one workgroup per row."""

@@ -12,11 +12,12 @@ namespace zi {
 template <bool NUC, bool CAP, typename T, int NV, bool M, bool PN>
 static hipError_t launch_sample_t(const SampleParams &P, int rows, hipStream_t st) {
     if (rows >= kRowLoopRows) {  // one workgroup per row fills the device
-        // min_p > 0 prefix: 32 elements per thread per step (the 64-element
-        // instances of this variant run out of registers)
-        constexpr int NVM = std::is_same<T, float>::value ? 8 : 4;
+        // min_p > 0: the streamed prefix (zi_prefix.hpp), eight 16-byte
+        // vectors per thread per step (four with a softcap or for masked bf16
+        // rows, whose extra state would not fit the registers beside eight)
+        constexpr int NVM = (CAP || (std::is_same<T, uint16_t>::value && M)) ? 4 : 8;
         if (NUC && P.min_p > 0.0f)
-            hipLaunchKernelGGL((row_kernel<T, NVM, M, PN, true, true, CAP>), dim3(rows), dim3(kThreads), 0, st, P);
+            hipLaunchKernelGGL((prefix_kernel<T, NVM, M, PN, CAP>), dim3(rows), dim3(kThreads), 0, st, P);
         else
             hipLaunchKernelGGL((row_kernel<T, NV, M, PN, NUC, false, CAP>), dim3(rows), dim3(kThreads), 0, st, P);
         return hipGetLastError();

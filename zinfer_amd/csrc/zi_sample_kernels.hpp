@@ -15,6 +15,7 @@
 
 #include "zi_launch.hpp"
 #include "zi_rowpass.hpp"
+#include "zi_prefix.hpp"
 #include "zi_tail.hpp"
 
 namespace zi {
@@ -238,17 +239,6 @@ __global__ __launch_bounds__(kThreads) void nucleus_kernel(SampleParams P) {
 // distinct: each holds the count of greater entries of the other list by a
 // binary search).  NUC: the prefix pass of whole-vocabulary rows, with the
 // row total accumulated over the chunks in each thread.
-
-// The whole-vocabulary prefix threshold for min_p > 0: an entry below it has
-// exp(x - M) < min_p for every maximum >= M, with room for the f32 rounding of
-// x - M and of the threshold itself (rounded down).  Monotone in M.
-__device__ __forceinline__ float minp_floor(float M, double ln_minp) {
-    const double d = (double)M + ln_minp - 0.01 - 1e-6 * fabs((double)M);
-    float t = (float)d;
-    if ((double)t > d) t = __uint_as_float(t > 0.0f ? __float_as_uint(t) - 1u : __float_as_uint(t) + 1u);
-    return t;
-}
-
 
 template <typename T, int NV, bool HAS_MASK, bool HAS_PEN, bool NUC, bool BY_MAX, bool CAP>
 __global__ __launch_bounds__(kThreads) void row_kernel(SampleParams P) {
