@@ -543,6 +543,8 @@ def bench_entropy(args, w):
     # per row: the logits and the draft id read; entropy, k ids, k probabilities, argmax, accept written
     nbytes = rows * (V * 4 + 4 + 4 + 8 * k + 4 + 1)
     achieved = nbytes / (ms * 1e-3) / 1e9
+    # batches whose chunked grid exceeds one workgroup per CU walk their segments
+    kname = "entropy_walk_kernel" if w.rows * _entropy_chunks(w.vocab, w.rows) > 256 else "entropy_kernel"
     print(json.dumps({
         "metric": "rows/sec + HBM GB/s (% of peak), 64x262144 f32 entropy + top-8 + accept",
         "value": round(rows / (ms * 1e-3), 1), "unit": "rows/s", "n_gpus": 1, "steps": steps,
@@ -552,11 +554,9 @@ def bench_entropy(args, w):
         "config": {"workload": w.name, "rows": rows, "vocab": V, "k": k, "rotating_input_sets": nsets,
                    "launch": "hip_graph_replay"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "algorithmic_bytes_per_launch": nbytes,
-                     # batches whose chunked grid exceeds one workgroup per CU walk their segments
-                     "kernel": "entropy_walk_kernel" if w.rows * _entropy_chunks(w.vocab, w.rows) > 256
-                     else "entropy_kernel"},
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "traffic": read_traffic(args.traffic, kname, w.name),
+                     "algorithmic_bytes_per_launch": nbytes, "kernel": kname},
         "cpu_baseline": cpu,
         "wall_s": round(wall, 3),
     }), flush=True)

@@ -19,7 +19,7 @@ static hipError_t launch_sample_t(const SampleParams &P, int rows, hipStream_t s
         if (NUC && P.min_p > 0.0f)
             hipLaunchKernelGGL((prefix_kernel<T, NVM, M, PN, CAP>), dim3(rows), dim3(kThreads), 0, st, P);
         else
-            hipLaunchKernelGGL((row_kernel<T, NV, M, PN, NUC, false, CAP>), dim3(rows), dim3(kThreads), 0, st, P);
+            hipLaunchKernelGGL((row_kernel<T, NV, M, PN, NUC, CAP>), dim3(rows), dim3(kThreads), 0, st, P);
         return hipGetLastError();
     }
     dim3 grid(rows * P.src.G), block(kThreads);

@@ -240,7 +240,7 @@ __global__ __launch_bounds__(kThreads) void nucleus_kernel(SampleParams P) {
 // binary search).  NUC: the prefix pass of whole-vocabulary rows, with the
 // row total accumulated over the chunks in each thread.
 
-template <typename T, int NV, bool HAS_MASK, bool HAS_PEN, bool NUC, bool BY_MAX, bool CAP>
+template <typename T, int NV, bool HAS_MASK, bool HAS_PEN, bool NUC, bool CAP>
 __global__ __launch_bounds__(kThreads) void row_kernel(SampleParams P) {
     __shared__ union {
         SampleStageA<T, NV, HAS_PEN> a;
@@ -252,7 +252,6 @@ __global__ __launch_bounds__(kThreads) void row_kernel(SampleParams P) {
     __shared__ int s_dig[2];
     __shared__ int s_n;
     __shared__ float s_wmax[kWaves];
-    __shared__ float s_wmax2[kWaves];
     __shared__ double s_ws[kWaves];
 
     const RowSource &a = P.src;
@@ -268,15 +267,6 @@ __global__ __launch_bounds__(kThreads) void row_kernel(SampleParams P) {
     if constexpr (HAS_PEN) pen = &sm.a.p.pen;
     float ref = -INFINITY, S = 0.0f;  // NUC: running sum exp(x - ref) of this thread's elements
     int n_run = 0, cur = 0;           // running list length and buffer (uniform)
-    // NUC with min_p > 0: the prefix is every entry above minp_floor(row max)
-    // (the reference's keep never passes the first entry below min_p), so
-    // each chunk's threshold trails the running maximum of the unpenalized
-    // stream values instead of a top-256 selection.  It is also kept at or
-    // below the second largest lane maximum seen, which the row's second
-    // largest entry (the margin) is not below.
-    constexpr bool by_max = NUC && BY_MAX;  // launched only when min_p > 0
-    const double ln_minp = by_max ? log((double)P.min_p) : 0.0;
-    float m_run = -INFINITY, m2_run = -INFINITY;  // two largest lane maxima so far (distinct lanes)
     // The row in steps of what the registers hold (the plan's chunking only
     // sets the layout of the row-total record below).
     constexpr int SUB = kThreads * NV * VecTraits<T>::VEC;
@@ -293,30 +283,7 @@ __global__ __launch_bounds__(kThreads) void row_kernel(SampleParams P) {
         chunk_stream<T, NV, HAS_MASK, HAS_PEN, CAP, NoHook, NV, NoMid, PF>(a, row, c0, c1, cr, pen, &own, NoHook(),
                                                                           NoMid(), pf, c1, min(a.V, c1 + SUB));
         float tau;
-        if constexpr (by_max) {
-            const float lm = cr.lmax;
-            const float wm = wave_max_f(lm);
-            const uint64_t top = ballot(lm == wm);
-            const float w2 = __popcll(top) >= 2 ? wm : wave_max_f(lm == wm ? -INFINITY : lm);
-            if (lane == 0) {
-                s_wmax[wid] = wm;
-                s_wmax2[wid] = w2;
-            }
-            if (tid == 0) s_n = 0;
-            if (tid < kSortMax) sm.a.sel.rank[tid] = 0u;
-            __syncthreads();
-#pragma unroll
-            for (int w = 0; w < 2 * kWaves; ++w) {
-                const float v = w < kWaves ? s_wmax[w] : s_wmax2[w - kWaves];
-                if (v > m_run) {
-                    m2_run = m_run;
-                    m_run = v;
-                } else if (v > m2_run) {
-                    m2_run = v;
-                }
-            }
-            tau = m_run == -INFINITY ? -INFINITY : fminf(minp_floor(m_run, ln_minp), m2_run);
-        } else if (n_run == k) {  // uniform: nothing below the running k-th value can enter
+        if (n_run == k) {  // uniform: nothing below the running k-th value can enter
             if (tid == 0) s_n = 0;
             if (tid < kSortMax) sm.a.sel.rank[tid] = 0u;
             __syncthreads();
@@ -394,25 +361,7 @@ __global__ __launch_bounds__(kThreads) void row_kernel(SampleParams P) {
         }
         return;
     }
-    int n = n_run;
-    bool complete = false;
-    if constexpr (by_max) {  // trim to the final threshold: the list is then a prefix of the row's order
-        const float mx = rl.val[cur][0];
-        const float tf = minp_floor(mx, ln_minp);
-        int m = 0;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const int i = lane + 64 * c;
-            m += __popcll(ballot(i < n_run && rl.val[cur][i] >= tf));
-        }
-        n = (mx == mx && mx != -INFINITY) ? max(m, min(2, n_run)) : n_run;  // the top two are exact
-        complete = m < k && mx == mx && mx != -INFINITY;  // nothing above tf was dropped by the cap
-        if (n < 2 && P.n_all >= 2) {  // fewer than two entries in the row: whole-order pass
-            if (tid == 0) P.nuc_flag[row] = 1;
-            return;
-        }
-    }
-    sample_tail<NUC>(P, row, rl.key[cur], rl.val[cur], n, sm.tl, u0, u1, tot, complete);
+    sample_tail<NUC>(P, row, rl.key[cur], rl.val[cur], n_run, sm.tl, u0, u1, tot);
 }
 
 }  // namespace zi
