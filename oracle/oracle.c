@@ -15,6 +15,84 @@
 
 float or_exp32(float x) { return (float)exp((double)x); }
 float or_log32(float x) { return (float)log((double)x); }
+
+/* The reference's f32 @exp (src/sampler.zig:219, 222, 230, 240; the softcap
+ * body, src/model.zig:2505).  The reference links no libc (build.zig:14), so
+ * @exp(f32) is a call to the Zig compiler runtime's expf, a port of musl's
+ * expf (FreeBSD e_expf.c).  Restated from that published algorithm, every step
+ * an f32 operation in the published order:
+ *   |x| > ln2/2 (0x3eb17218): k = (int)(invln2*x + (x < 0 ? -0.5 : 0.5)), or
+ *     k = +-1 when |x| <= 1.5 ln2 (0x3f851592); hi = x - k*ln2hi (exact),
+ *     lo = k*ln2lo, x = hi - lo;
+ *   |x| > 2^-13 (0x39000000): k = 0, hi = x, lo = 0;  else return 1 + x;
+ *   c = x - x^2*(P1 + x^2*P2);  y = 1 + (x*c/(2 - c) - lo + hi);
+ *   return k ? scalbnf(y, k) : y   (scalbnf: one rounding).
+ * Special cases: NaN -> NaN, x >= 88.722839 (0x42b17218) -> inf, x <=
+ * -103.972084 (0x42cff1b5) -> 0.  Pinned by tests/test_oracle_expf.py (error
+ * within 1 ulp of exp over dense grids, the special cases and boundaries, and
+ * the branch identities); that Zig 0.17.1's compiler runtime still carries
+ * this port is not checkable here (no Zig toolchain). */
+static float zf(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+static uint32_t zb(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+
+static float or_scalbnf(float y, int n) {
+    if (n > 127) {
+        y *= 0x1p127f;
+        n -= 127;
+        if (n > 127) {
+            y *= 0x1p127f;
+            n -= 127;
+            if (n > 127) n = 127;
+        }
+    } else if (n < -126) {
+        y *= 0x1p-102f;
+        n += 102;
+        if (n < -126) {
+            y *= 0x1p-102f;
+            n += 102;
+            if (n < -126) n = -126;
+        }
+    }
+    return y * zf((uint32_t)(0x7f + n) << 23);
+}
+
+float or_zexpf(float x) {
+    const float half[2] = {0.5f, -0.5f};
+    const float ln2hi = zf(0x3f317200u), ln2lo = zf(0x35bfbe8eu), invln2 = zf(0x3fb8aa3bu);
+    const float P1 = 11184783.0f * 0x1p-26f;  /* 0xaaaa8f.0p-26 */
+    const float P2 = -11883029.0f * 0x1p-32f; /* -0xb55215.0p-32 */
+    uint32_t hx = zb(x);
+    const int sign = (int)(hx >> 31);
+    hx &= 0x7fffffffu;
+    if (hx >= 0x42aeac50u) {
+        if (hx > 0x7f800000u) return x;
+        if (hx >= 0x42b17218u && !sign) return x * 0x1p127f;
+        if (sign && hx >= 0x42cff1b5u) return 0.0f;
+    }
+    int k;
+    float hi, lo;
+    if (hx > 0x3eb17218u) {
+        if (hx > 0x3f851592u) k = (int)(invln2 * x + half[sign]);
+        else k = 1 - sign - sign;
+        hi = x - (float)k * ln2hi;
+        lo = (float)k * ln2lo;
+        x = hi - lo;
+    } else if (hx > 0x39000000u) {
+        k = 0;
+        hi = x;
+        lo = 0.0f;
+    } else {
+        return 1.0f + x;
+    }
+    const float xx = x * x;
+    const float c = x - xx * (P1 + xx * P2);
+    const float y = 1.0f + (x * c / (2.0f - c) - lo + hi);
+    return k == 0 ? y : or_scalbnf(y, k);
+}
+
+void or_zexpf_array(const float *x, float *y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = or_zexpf(x[i]);
+}
 /* std.math.tanh(f32) (model.zig:2512, the softcap's scalar tail), as the f64
  * tanh rounded once to f32: within half an ulp plus the f64 error, the same
  * footing as or_exp32. */
@@ -102,7 +180,7 @@ void or_params_default(or_params *p) {
 /* The final-logit softcap of src/model.zig:2492-2510 (the vectorized body,
  * i < 32*floor(V/32)): z = l * (1/cap) with 1/cap in f32, clamped to [-9, 9],
  * e = exp(2z), tanh = (e - 1) / (e + 1), l = cap * tanh.  Every sequence step
- * rounds to f32; exp is or_exp32. */
+ * rounds to f32; exp is or_zexpf (the reference's expf). */
 /* The scalar tail of the same loop (model.zig:2511-2513, ids >= 32*floor(V/32)):
  * l = cap * tanh(l / cap), a true division and no clamp, so -inf maps to -cap
  * (the body maps it to -cap*tanh(9)). */
@@ -112,7 +190,7 @@ float or_softcap(float l, float cap) {
     const float inv_cap = 1.0f / cap;
     /* @min(@max(z, -9), 9) lowers to maxnum/minnum: a NaN operand yields the other */
     const float z = fminf(fmaxf(l * inv_cap, -9.0f), 9.0f);
-    const float e2z = or_exp32(z * 2.0f);
+    const float e2z = or_zexpf(z * 2.0f);
     const float t = (e2z - 1.0f) / (e2z + 1.0f);
     return cap * t;
 }
@@ -372,23 +450,23 @@ or_result or_sample_penalized(const or_params *p, const float *logits, uint32_t 
     uint32_t keep = n; /* :215-228 */
     if (p->top_p < 1.0f) {
         float total = 0.0f;
-        for (uint32_t i = 0; i < n; ++i) total += or_exp32(c[i].v - mx);
+        for (uint32_t i = 0; i < n; ++i) total += or_zexpf(c[i].v - mx);
         float acc = 0.0f;
         for (uint32_t i = 0; i < n; ++i) {
-            acc += or_exp32(c[i].v - mx);
+            acc += or_zexpf(c[i].v - mx);
             if (acc >= p->top_p * total) { keep = i + 1; break; }
         }
     }
     if (p->min_p > 0.0f) { /* :229-234 */
         for (uint32_t i = 0; i < keep; ++i)
-            if (or_exp32(c[i].v - mx) < p->min_p) { keep = i > 1 ? i : 1; break; }
+            if (or_zexpf(c[i].v - mx) < p->min_p) { keep = i > 1 ? i : 1; break; }
     }
 
     float inv_t = 1.0f / p->temp; /* :236-242 */
     float total = 0.0f;
     float *w = g_w;
     for (uint32_t i = 0; i < keep; ++i) {
-        w[i] = or_exp32((c[i].v - mx) * inv_t);
+        w[i] = or_zexpf((c[i].v - mx) * inv_t);
         total += w[i];
     }
 

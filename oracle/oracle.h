@@ -55,10 +55,22 @@
  *   or_softcap_tail        pinned: within two f32 ulps of cap*tanh(fl(l/cap)) in f64,
  *                          odd, +-inf -> +-cap, and applied to exactly the ids at
  *                          and above 32*floor(V/32) (tests/test_oracle_properties.py).
- *   exp, tanh              Zig @exp (compiler-rt expf) and std.math.tanh last-ulp
- *                          bits are PARITY UNPINNED; this oracle and the device use
- *                          (float)exp((double)x) and (float)tanh((double)x),
- *                          correctly rounded in practice.
+ *   or_zexpf               the reference's @exp(f32) on the sampling path: the
+ *                          compiler runtime's expf (the reference links no libc),
+ *                          a port of musl's / FreeBSD's expf, restated from that
+ *                          published algorithm.  Pinned (tests/test_oracle_expf.py):
+ *                          within 1 ulp of exp over dense grids (subnormal results
+ *                          included), the special values and thresholds, the
+ *                          |x| <= 2^-13 branch (1 + x), both sides of the reduction
+ *                          branches' boundaries, and not correctly rounded (it is
+ *                          not the f64-rounded exp; planting an f64 evaluation or a
+ *                          perturbed P2 fails the tests).  That Zig 0.17.1's
+ *                          runtime still ships this port is not checkable here (no
+ *                          Zig toolchain).
+ *   tanh, pow's exp/log    std.math.tanh (softcap tail) and std.math.pow's exp/log
+ *                          last-ulp bits are PARITY UNPINNED; the oracle and the
+ *                          device use (float)tanh((double)x), (float)exp((double)x)
+ *                          and (float)log((double)x), correctly rounded in practice.
  */
 #ifndef ZINFER_ORACLE_H
 #define ZINFER_ORACLE_H
@@ -110,6 +122,8 @@ typedef struct or_sample_diag {
 } or_sample_diag;
 
 float or_exp32(float x);
+float or_zexpf(float x);
+void or_zexpf_array(const float *x, float *y, int64_t n);
 float or_log32(float x);
 float or_tanh32(float x);
 float or_pow_zig(float x, float y);

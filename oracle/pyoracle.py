@@ -99,6 +99,10 @@ def lib():
         f32p, u32p = C.POINTER(C.c_float), C.POINTER(C.c_uint32)
         L.or_softcap.restype = C.c_float
         L.or_softcap.argtypes = [C.c_float, C.c_float]
+        L.or_zexpf.restype = C.c_float
+        L.or_zexpf.argtypes = [C.c_float]
+        L.or_zexpf_array.restype = None
+        L.or_zexpf_array.argtypes = [C.c_void_p, C.c_void_p, C.c_int64]
         L.or_exp32.restype = C.c_float
         L.or_exp32.argtypes = [C.c_float]
         L.or_tanh32.restype = C.c_float
@@ -183,7 +187,21 @@ def tanh32(x: float) -> float:
 
 
 def exp32(x: float) -> float:
+    """(float)exp((double)x): the correctly rounded stand-in kept for pow."""
     return lib().or_exp32(float(x))
+
+
+def zexpf(x: float) -> float:
+    """The reference's @exp(f32) (compiler-rt expf, oracle.c or_zexpf)."""
+    return lib().or_zexpf(float(x))
+
+
+def zexpf_array(x) -> np.ndarray:
+    """or_zexpf over a float32 array."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    lib().or_zexpf_array(x.ctypes.data, y.ctypes.data, x.size)
+    return y
 
 
 def pow_zig(x: float, y: float) -> float:

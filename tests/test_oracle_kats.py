@@ -68,7 +68,7 @@ def test_xtc_keeps_top_choice_without_alternative(oracle):
                       xtc_min_keep=1)
     logits = np.full(10, -50.0, np.float32)
     logits[0], logits[1] = 10.0, 6.0
-    total = np.float32(1.0) + np.float32(oracle.exp32(-4.0))
+    total = np.float32(1.0) + np.float32(oracle.zexpf(-4.0))
     for u in np.linspace(0, 1, 2001, endpoint=False, dtype=np.float32):
         tok, _, diag = oracle.sample_row(p, logits, [0.5, u])
         assert diag["ndraws"] == 2 and diag["start"] == 0

@@ -7,7 +7,10 @@ import pytest
 
 
 def exp32(x):
-    return np.float32(np.exp(np.float64(np.float32(x))))
+    """The reference's @exp(f32) (oracle/or_zexpf, pinned in test_oracle_expf.py)."""
+    from oracle import pyoracle
+
+    return np.float32(pyoracle.zexpf(float(np.float32(x))))
 
 
 # ------------------------------------------------------------------ top-k

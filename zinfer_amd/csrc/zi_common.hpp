@@ -15,6 +15,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "zi_expf.hpp"
+
 namespace zi {
 
 constexpr int kThreads = 512;
@@ -38,9 +40,12 @@ __device__ __forceinline__ uint64_t ckey(float v, uint32_t id) {
 
 __device__ __forceinline__ uint32_t ckey_id(uint64_t k) { return ~(uint32_t)(k & 0xFFFFFFFFull); }
 
-// Correctly rounded in practice: f64 exp rounded once to f32.  Used wherever a
-// result must agree bit-for-bit with the CPU oracle (oracle/or_exp32).
-__device__ __forceinline__ float exp32(float x) { return (float)exp((double)x); }
+// The reference's f32 exp (its compiler runtime's expf, zi_expf.hpp), used
+// wherever the reference evaluates @exp on f32: the sampler's terms and
+// weights and the softcap body.  The branch-free form, which gives the same
+// bits for every input; the CPU oracle evaluates the published steps
+// (oracle/or_zexpf).
+__device__ __forceinline__ float exp32(float x) { return zexpf_nb(x); }
 
 // Final-logit softcap, the vectorized body of src/model.zig:2492-2510:
 // z = l * (1/cap) clamped to [-9, 9], tanh = (e - 1) / (e + 1) with e = exp(2z),

@@ -14,6 +14,7 @@
 #include "../../include/zinfer_hip.h"
 #include "zi_internal.hpp"
 #include "zi_launch.hpp"
+#include "zi_expf.hpp"
 #include "zi_pow.hpp"
 
 namespace {
@@ -72,7 +73,7 @@ static void host_softcap(float *logits, uint32_t V, float cap) {
     const uint32_t body = V / 32 * 32;
     for (uint32_t i = 0; i < body; ++i) {
         const float z = std::fmin(std::fmax(logits[i] * inv_cap, -9.0f), 9.0f);
-        const float e2z = (float)std::exp((double)(z * 2.0f));
+        const float e2z = zi::zexpf(z * 2.0f);
         logits[i] = cap * ((e2z - 1.0f) / (e2z + 1.0f));
     }
     for (uint32_t i = body; i < V; ++i) logits[i] = cap * (float)std::tanh((double)(logits[i] / cap));

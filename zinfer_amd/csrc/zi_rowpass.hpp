@@ -51,6 +51,26 @@ __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70)
 // Returns true in exactly one workgroup of the row (the last to finish);
 // every thread's agent-scope stores are performed before the ticket moves.
 // The last workgroup re-arms the ticket for the next launch.
+//
+// Why the last workgroup sees every other workgroup's list:
+//  1. Producers write their lists with agent-scope stores (sc1), which are
+//     performed at the device's coherence point, not only in the XCD's L2.
+//  2. wait_vmem() is s_waitcnt vmcnt(0): on gfx950 vmcnt counts stores as
+//     well as loads, and a store leaves the count only once it is performed
+//     at the scope its cache bits ask for.  After it, this thread's stores are
+//     performed.
+//  3. __syncthreads() (a workgroup fence, so the compiler moves no memory
+//     operation across it, and s_barrier) puts every thread's step 2 before
+//     thread 0's ticket increment, an agent-scope atomic performed at the
+//     coherence point.
+//  4. The increments of one row are totally ordered at that point: the
+//     workgroup that reads G - 1 comes after the other G - 1 increments,
+//     each of which came after its workgroup's stores.
+//  5. The consumer reads the lists with agent-scope loads (sc1: they miss in
+//     its own L2 rather than hit a stale line) issued after the ticket's
+//     result, through *s_flag and a barrier, so none is issued early.
+// The re-armed ticket (0) is read by the next launch only, after the kernel
+// boundary.
 __device__ __forceinline__ bool row_ticket(int32_t *tickets, int row, int G, int *s_flag) {
     wait_vmem();
     __syncthreads();
