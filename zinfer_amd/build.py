@@ -21,7 +21,7 @@ CONSUMER_SRC = os.path.join(ROOT, "tests", "capi", "consumer.c")
 CONSUMER = os.path.join(ROOT, "tests", "capi", "zi_consumer")
 OBJ = os.path.join(ROOT, "_build", "obj")
 
-SOURCES = ["zi_sample.hip", "zi_sample_cap.hip", "zi_exact.hip", "zi_argmax.hip", "zi_entropy.hip", "zi_grammar.hip", "zi_pruned.hip", "zi_dry.hip",
+SOURCES = ["zi_sample.hip", "zi_sample_cap.hip", "zi_exact.hip", "zi_whole.hip", "zi_argmax.hip", "zi_entropy.hip", "zi_grammar.hip", "zi_pruned.hip", "zi_dry.hip",
            "zi_api.cpp",
            "zi_host.cpp"]
 

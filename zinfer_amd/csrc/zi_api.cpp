@@ -414,6 +414,15 @@ static int32_t run_whole_order(zi_ctx *c, const zi_params *p, const zi_batch *b,
     X.key1 = c->ex_sort + 3 * plane;
     X.id1 = c->ex_sort + 4 * plane;
     X.ldk = c->ex_ld;
+    // bf16 rows without a softcap, XTC or candidate outputs: the flagged rows
+    // go through the sort-free pass first; what it cannot take (or any other
+    // row) stays flagged for the sorting pass
+    const bool xtc = p->xtc_probability > 0.0f && p->xtc_threshold <= 0.5f;
+    if (whole && b->dtype == ZI_BF16 && src.cap <= 0.0f && !xtc && !out->cand_ids && !out->cand_vals &&
+        !out->probs) {
+        hipError_t ew = zi::launch_whole(X, b->rows, c->stream);
+        if (ew != hipSuccess) return zi_hip_fail(ew, "whole-order kernel launch");
+    }
     hipError_t e = zi::launch_exact(X, b->dtype, b->rows, c->stream);
     if (e != hipSuccess) return zi_hip_fail(e, "exact kernel launch");
     return ZI_OK;

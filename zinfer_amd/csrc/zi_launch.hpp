@@ -88,7 +88,7 @@ struct ExactParams {
     float *cand_vals;
     float *probs;
     int cand_ld;
-    const int32_t *flags;  // [rows]: row r runs iff flags[r] != 0; NULL: every row
+    int32_t *flags;        // [rows]: row r runs iff flags[r] != 0; NULL: every row (whole_kernel clears it)
     const double *g_stat;  // [rows][G][3] chunk (max, sum exp(x - max)) of the prefix pass, or NULL
     int n_all;             // V when g_stat bounds the whole-vocabulary total
     uint32_t *keys, *key0, *id0, *key1, *id1;  // scratch [rows][ldk]: keys in id order, sort buffers
@@ -145,6 +145,8 @@ hipError_t launch_pruned_fill(const void *logits, void *dense, int64_t ld, int64
 hipError_t launch_sample_capped(const SampleParams &P, int dtype, int nv, int rows, hipStream_t st);
 hipError_t launch_nucleus_capped(const SampleParams &P, int dtype, int nv, int rows, hipStream_t st);
 hipError_t launch_exact(const ExactParams &P, int dtype, int rows, hipStream_t st);
+// bf16 whole-vocabulary rows without a sort (zi_whole.hip); flags required.
+hipError_t launch_whole(const ExactParams &P, int rows, hipStream_t st);
 hipError_t launch_argmax(const ArgmaxParams &P, int dtype, int nv, int rows, hipStream_t st);
 hipError_t launch_entropy(const EntropyParams &P, int dtype, int nv, int rows, hipStream_t st);
 // G segments per row, each walked by one workgroup (entropy_walk_kernel).

@@ -1,0 +1,580 @@
+// zi_whole.hip -- whole-order sampling of bf16 rows without a sort:
+// Sampler.sampleWithMargin (src/sampler.zig:190-276) with k = V (the
+// std.mem.sort branch, :198-202) for the rows the prefix pass flagged, in
+// O(V + distinct values) per row.
+//
+// A bf16 row holds at most 65536 distinct values, and only those within
+// fl(x - mx) >= -16.75 (terms >= 2^-24; below it a term changes no sequential
+// sum, every prefix being >= 1) or above the min-p floor can matter.  So the
+// order the reference sorts is a list of groups (value, count) in descending
+// value, and every sum of the tail is walked over the groups exactly
+// (zi_walk.hpp).  Only the drawn entry's position needs its id: among the
+// entries of its value, ascending id (the stable sort's tie rule).
+//
+// One 512-thread workgroup per flagged row:
+//  1. penalty bitset and hash in LDS; each penalized id's first inserter
+//     loads its logit (as in the prefix pass).
+//  2. read the row: the row max and second value, and a bitmap of the 16-bit
+//     order keys present among the unpenalized entries.
+//  3. the penalized values; the floor; ranks of the present keys at or above
+//     it (descending) from a suffix count over the bitmap words.
+//  4. read the row again: each entry's key rank gets a count.
+//  5. the group list: key groups and penalized entries (one group each)
+//     merged by value.
+//  6. wave 0 walks the groups: the top-p total and crossing, min-p, the
+//     temperature total over keep, the draw.
+//  7. the drawn entry's id: the (j+1)-th entry, in id order, of its value.
+// A row with more distinct values above the floor than the group list holds,
+// a non-finite maximum, or no selectable entry keeps its flag, and the
+// sorting pass (zi_exact.hip) runs it.
+#include "zi_launch.hpp"
+#include "zi_rowpass.hpp"
+#include "zi_walk.hpp"
+
+namespace zi {
+
+constexpr int kWholeKeys = 4096;                   // distinct bf16 values above the floor
+constexpr int kWholePen = kOwnSlots * kThreads;    // penalized entries (window + edits), one per owner slot
+constexpr int kWholeGroups = kWholeKeys + kWholePen;
+
+struct WholeLds {
+    uint32_t pbits[kMaxVocab / 32];  // penalized ids
+    union {
+        struct {  // steps 1-3
+            uint32_t key[kHashMax];
+            uint32_t cnt[kHashMax];
+            float delta[kHashMax];
+        } h;
+        struct {  // steps 5-7
+            float gval[kWholeGroups];
+            uint32_t gcnt[kWholeGroups];
+        } g;
+    } u;
+    uint32_t kbits[65536 / 32];  // present keys
+    uint32_t wsuf[65536 / 32];   // present keys (at or above the floor) in words above each word
+    uint32_t bcnt[kWholeKeys];   // entries per key rank
+    uint16_t bkey[kWholeKeys];   // key of each rank
+    float pval[kWholePen];       // penalized entries: value, id (then sorted by value desc, id asc)
+    uint32_t pid[kWholePen];
+    float sval[kWholePen];
+    uint32_t sid[kWholePen];
+    float wt1[kWaves], wt2[kWaves];
+    uint32_t wsum[kWaves];
+    int npen, nsel;
+    int found;
+    uint32_t tok;
+    float f[4];
+    int64_t i64[4];
+};
+
+// bf16 order key: the high half of okey (exact for bf16 values: their low
+// halves are one constant per sign), and back.
+__device__ __forceinline__ uint32_t key16(float v) { return okey(v) >> 16; }
+__device__ __forceinline__ float key16_value(uint32_t k) {
+    return (k & 0x8000u) ? __uint_as_float((k & 0x7FFFu) << 16) : __uint_as_float(((~k) & 0xFFFFu) << 16);
+}
+
+// The smallest float f with every x >= f having fl(x - mx) >= dlo (a value a
+// little below mx + dlo, rounded down; a lower floor only keeps more).
+__device__ __forceinline__ float whole_floor(float mx, float dlo) {
+    const double d = (double)mx + (double)dlo - (fabs((double)mx) + fabs((double)dlo)) * 1e-6;
+    float f = (float)d;
+    if ((double)f > d) f = __uint_as_float(__float_as_uint(f) + (f > 0.0f ? -1 : 1));
+    return f;
+}
+
+__device__ __forceinline__ void top2_merge(float &t1, float &t2, float x) {
+    t2 = fmaxf(t2, fminf(t1, x));
+    t1 = fmaxf(t1, x);
+}
+
+__device__ __forceinline__ uint64_t min_u64(uint64_t a, uint64_t b) { return a < b ? a : b; }
+
+__device__ __forceinline__ uint64_t shfl_up_u64(uint64_t v, int o) {
+    const uint32_t lo = __shfl_up((uint32_t)v, o), hi = __shfl_up((uint32_t)(v >> 32), o);
+    return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l) {
+    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, l), hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), l);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// One wave walks groups [0, G) over their first `limit` entries (every lane
+// active, uniform result).  Returns the entry index at which the walk stops
+// (group *sg, copy *sc), or -1; v is the running value.
+template <class Term>
+__device__ int64_t walk_groups(const float *gval, const uint32_t *gcnt, int G, uint64_t limit, Term term, int mode,
+                               float thr, float &v, int *sg, int64_t *sc) {
+    const int lane = threadIdx.x & 63;
+    int g = 0;
+    uint64_t cum = 0;
+    while (g < G && cum < limit) {
+        if ((mode != kWalkDrop && v == 0.0f) || (mode == kWalkDrop && !(v > 0.0f))) {  // no grid yet: one group
+            const uint64_t c = min_u64((uint64_t)gcnt[g], limit - cum);
+            const int64_t s = walk_group(v, term(gval[g]), c, mode, thr);
+            if (s >= 0) {
+                *sg = g;
+                *sc = s;
+                return (int64_t)cum + s;
+            }
+            cum += c;
+            ++g;
+            continue;
+        }
+        const WalkGrid gr = walk_grid(v);
+        const uint32_t p0 = gr.m & 1u;
+        const int gl = g + lane;
+        const uint32_t craw = gl < G ? gcnt[gl] : 0u;
+        uint32_t cin = craw;  // inclusive prefix of the raw counts
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t y = __shfl_up(cin, o);
+            if (lane >= o) cin += y;
+        }
+        const uint64_t before = cum + (cin - craw);
+        const uint32_t c = before >= limit ? 0u : (uint32_t)min_u64((uint64_t)craw, limit - before);
+        const float t = c ? term(gval[gl]) : 0.0f;
+        WalkMap mp = walk_map(walk_term(t, gr.qe), c);
+        uint32_t par = mp.par0 | (mp.par1 << 1);
+        uint32_t ccl = c;  // inclusive prefix of the clamped counts
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {  // inclusive scan: earlier lanes' map, then this lane's
+            WalkMap pm;
+            pm.inc0 = shfl_up_u64(mp.inc0, o);
+            pm.inc1 = shfl_up_u64(mp.inc1, o);
+            const uint32_t pp = __shfl_up(par, o);
+            pm.par0 = pp & 1u;
+            pm.par1 = pp >> 1;
+            const uint32_t yc = __shfl_up(ccl, o);
+            if (lane >= o) {
+                mp = walk_compose(pm, mp);
+                par = mp.par0 | (mp.par1 << 1);
+                ccl += yc;
+            }
+        }
+        const uint64_t P = p0 ? mp.inc1 : mp.inc0;
+        const bool ev = c > 0 && walk_event(gr.m, gr.qe, P, mode, thr);
+        const uint64_t b = ballot(ev);
+        if (!b) {
+            const uint64_t P63 = readlane_u64(P, 63);
+            v = walk_value(mode == kWalkDrop ? gr.m - P63 : gr.m + P63, gr.qe);
+            cum += (uint32_t)__builtin_amdgcn_readlane(ccl, 63);
+            g += 64;
+            continue;
+        }
+        const int L = __ffsll((unsigned long long)b) - 1;
+        const uint64_t Pp = L > 0 ? readlane_u64(P, L - 1) : 0;
+        const uint32_t cp = L > 0 ? (uint32_t)__builtin_amdgcn_readlane(ccl, L - 1) : 0u;
+        v = walk_value(mode == kWalkDrop ? gr.m - Pp : gr.m + Pp, gr.qe);
+        cum += cp;
+        const float tL = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), L));
+        const uint32_t cL = (uint32_t)__builtin_amdgcn_readlane(c, L);
+        const int64_t s = walk_group(v, tL, cL, mode, thr);
+        if (s >= 0) {
+            *sg = g + L;
+            *sc = s;
+            return (int64_t)cum + s;
+        }
+        cum += cL;
+        g += L + 1;
+    }
+    return -1;
+}
+
+template <bool HAS_MASK, bool HAS_PEN>
+__global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
+    __shared__ WholeLds L;
+    const RowSource &a = P.src;
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int row = blockIdx.x;
+    if (P.flags[row] == 0) return;  // settled by the prefix pass (uniform)
+    const int V = a.V;
+    constexpr int VEC = 8;
+    const int nvec = (V + VEC - 1) / VEC;
+    const uint16_t *lrow = reinterpret_cast<const uint16_t *>(a.logits) + (int64_t)row * a.ld;
+    const uint32_t *mrow = HAS_MASK ? a.mask + (int64_t)row * a.mask_ld : nullptr;
+
+    // 1. penalties: bitset, hash, owners
+    uint32_t oid[kOwnSlots];
+    int oslot[kOwnSlots];
+    uint32_t oraw[kOwnSlots];
+#pragma unroll
+    for (int s = 0; s < kOwnSlots; ++s) {
+        oid[s] = 0xFFFFFFFFu;
+        oslot[s] = 0;
+        oraw[s] = 0u;
+    }
+    RowPen rp;
+    rp.hs_log2 = 6;
+    if constexpr (HAS_PEN) {
+        PenRegs pr;
+        pen_prefetch(a, row, pr);
+        rp = row_pen(a, row);
+        pen_window(rp, pr);
+        for (int i = tid; i < (V + 31) / 32; i += kThreads) L.pbits[i] = 0u;
+        for (int i = tid; i < kHashMax; i += kThreads) {
+            L.u.h.key[i] = 0u;
+            L.u.h.cnt[i] = 0u;
+            L.u.h.delta[i] = 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < kOwnSlots; ++s) {
+            const uint32_t id = s < kWinPerThread ? pr.w[s] : pr.e;
+            if (id < (uint32_t)V) {
+                const uint32_t bit = 1u << (id & 31);
+                const bool first = !(atomicOr(&L.pbits[id >> 5], bit) & bit);
+                const int h = pen_insert(L.u.h, id, rp.hs_log2);
+                if (s < kWinPerThread) atomicAdd(&L.u.h.cnt[h], 1u);
+                else L.u.h.delta[h] = pr.d;
+                if (first) {
+                    oid[s] = id;
+                    oslot[s] = h;
+                }
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < kOwnSlots; ++s)
+            if (oid[s] != 0xFFFFFFFFu) oraw[s] = (uint32_t)lrow[oid[s]];
+    }
+    for (int i = tid; i < 65536 / 32; i += kThreads) L.kbits[i] = 0u;
+    if (tid == 0) {
+        L.npen = 0;
+        L.nsel = 0;
+        L.found = 0;
+    }
+    __syncthreads();
+
+    // 2. row max / second (unpenalized entries), present keys
+    float t1 = -INFINITY, t2 = -INFINITY;
+    for (int q = tid; q < nvec; q += kThreads) {
+        const uint4 raw = *reinterpret_cast<const uint4 *>(lrow + q * VEC);
+        float v[VEC];
+        unpack<uint16_t>(raw, v);
+        const int id0 = q * VEC;
+        const uint32_t mb = HAS_MASK ? mrow[id0 >> 5] >> (id0 & 31) : 0xFFu;
+        const uint32_t pb = HAS_PEN ? (L.pbits[id0 >> 5] >> (id0 & 31)) : 0u;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+            if (id0 + e >= V || ((pb >> e) & 1u)) continue;
+            float x = v[e];
+            if (HAS_MASK && !((mb >> e) & 1u)) x = -INFINITY;
+            if (x != x) continue;  // NaN: no place in the order (outside the reference's contract)
+            top2_merge(t1, t2, x);
+            const uint32_t k = key16(x);
+            const uint32_t bit = 1u << (k & 31);
+            if (!(L.kbits[k >> 5] & bit)) atomicOr(&L.kbits[k >> 5], bit);
+        }
+    }
+    // 3. penalized values
+    float pvs[kOwnSlots];
+#pragma unroll
+    for (int s = 0; s < kOwnSlots; ++s) {
+        pvs[s] = __builtin_nanf("");
+        if (HAS_PEN && oid[s] != 0xFFFFFFFFu) {
+            float x = __uint_as_float(oraw[s] << 16);
+            if (HAS_MASK && !((mrow[oid[s] >> 5] >> (oid[s] & 31)) & 1u)) x = -INFINITY;
+            x = pen_apply(x, L.u.h.cnt[oslot[s]], L.u.h.delta[oslot[s]], a);
+            pvs[s] = x;
+            if (x == x) top2_merge(t1, t2, x);
+        }
+    }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const float o1 = __shfl_xor(t1, o), o2 = __shfl_xor(t2, o);
+        t2 = fmaxf(fmaxf(t2, o2), fminf(t1, o1));
+        t1 = fmaxf(t1, o1);
+    }
+    if (lane == 0) {
+        L.wt1[wid] = t1;
+        L.wt2[wid] = t2;
+    }
+    __syncthreads();  // maxima; every read of the hash is done
+    float mx = L.wt1[0], second = L.wt2[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) {
+        const float o1 = L.wt1[w], o2 = L.wt2[w];
+        second = fmaxf(fmaxf(second, o2), fminf(mx, o1));
+        mx = fmaxf(mx, o1);
+    }
+    if (!__builtin_isfinite(mx)) return;  // the sorting pass handles it (uniform)
+    // the floor: entries below it cannot reach keep nor change a sum
+    float fv = -INFINITY;
+    if (P.top_p < 1.0f) fv = whole_floor(mx, -16.75f);
+    else if (P.min_p > 0.0f) fv = whole_floor(mx, fminf(logf(P.min_p) - 0.01f, 0.0f));
+    uint32_t kmin = fv == -INFINITY ? 0u : key16(fv);
+    if (fv != -INFINITY && key16_value(kmin) < fv) ++kmin;  // first key whose value is >= fv
+#pragma unroll
+    for (int s = 0; s < kOwnSlots; ++s) {  // penalized entries at or above the floor
+        if (pvs[s] == pvs[s] && pvs[s] >= fv) {
+            const int i = atomicAdd(&L.npen, 1);
+            L.pval[i] = pvs[s];
+            L.pid[i] = oid[s];
+        }
+    }
+    // key ranks: present keys >= kmin, descending; each thread sums 4 words
+    uint32_t wc[4], mine = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t w = (uint32_t)(4 * tid + j);
+        uint32_t bits = L.kbits[w];
+        if (w * 32 + 31 < kmin) bits = 0u;
+        else if (w * 32 < kmin) bits &= ~0u << (kmin - w * 32);
+        L.kbits[w] = bits;
+        wc[j] = (uint32_t)__popc(bits);
+        mine += wc[j];
+    }
+    // suffix over threads (descending keys: higher threads first)
+    uint32_t incl = mine;  // inclusive over higher-or-equal lanes within the wave
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t y = __shfl_down(incl, o);
+        if (lane + o < 64) incl += y;
+    }
+    if (lane == 0) L.wsum[wid] = incl;
+    __syncthreads();
+    uint32_t above = incl - mine;  // in higher lanes of this wave
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w)
+        if (w > wid) above += L.wsum[w];
+    uint32_t D = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) D += L.wsum[w];
+    const int npen = L.npen;
+    if (D > (uint32_t)kWholeKeys) return;  // too many distinct values: the sorting pass (uniform)
+#pragma unroll
+    for (int j = 3; j >= 0; --j) {  // words in descending order within this thread
+        const uint32_t w = (uint32_t)(4 * tid + j);
+        L.wsuf[w] = above;
+        uint32_t bits = L.kbits[w];
+        uint32_t r = above;
+        while (bits) {  // highest key first
+            const int b = 31 - __clz(bits);
+            L.bkey[r] = (uint16_t)(w * 32 + (uint32_t)b);
+            L.bcnt[r] = 0u;
+            ++r;
+            bits &= ~(1u << b);
+        }
+        above += wc[j];
+    }
+    __syncthreads();
+
+    // 4. counts per key rank
+    for (int q = tid; q < nvec; q += kThreads) {
+        const uint4 raw = *reinterpret_cast<const uint4 *>(lrow + q * VEC);
+        float v[VEC];
+        unpack<uint16_t>(raw, v);
+        const int id0 = q * VEC;
+        const uint32_t mb = HAS_MASK ? mrow[id0 >> 5] >> (id0 & 31) : 0xFFu;
+        const uint32_t pb = HAS_PEN ? (L.pbits[id0 >> 5] >> (id0 & 31)) : 0u;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+            if (id0 + e >= V || ((pb >> e) & 1u)) continue;
+            float x = v[e];
+            if (HAS_MASK && !((mb >> e) & 1u)) x = -INFINITY;
+            if (x != x) continue;
+            const uint32_t k = key16(x);
+            if (k < kmin) continue;
+            const uint32_t w = k >> 5, above_in = L.kbits[w] >> (k & 31) >> 1;
+            atomicAdd(&L.bcnt[L.wsuf[w] + (uint32_t)__popc(above_in)], 1u);
+        }
+    }
+    // penalized entries ranked by (value desc, id asc)
+    for (int i = tid; i < npen; i += kThreads) {
+        const float vi = L.pval[i];
+        const uint32_t ii = L.pid[i];
+        int r = 0;
+        for (int j = 0; j < npen; ++j) {
+            const float vj = L.pval[j];
+            r += (vj > vi || (vj == vi && L.pid[j] < ii)) ? 1 : 0;
+        }
+        L.sval[r] = vi;
+        L.sid[r] = ii;
+    }
+    __syncthreads();
+
+    // 5. the group list, key groups and penalized entries merged by value
+    //    (a key group before the penalized entries of its value)
+    for (int r = tid; r < (int)D; r += kThreads) {
+        const float vr = key16_value(L.bkey[r]);
+        int lo = 0, hi = npen;  // penalized entries with value > vr
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (L.sval[mid] > vr) lo = mid + 1;
+            else hi = mid;
+        }
+        L.u.g.gval[r + lo] = vr;
+        L.u.g.gcnt[r + lo] = L.bcnt[r];
+    }
+    for (int p = tid; p < npen; p += kThreads) {
+        const float vp = L.sval[p];
+        int lo = 0, hi = (int)D;  // key groups with value >= vp
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (key16_value(L.bkey[mid]) >= vp) lo = mid + 1;
+            else hi = mid;
+        }
+        L.u.g.gval[p + lo] = vp;
+        L.u.g.gcnt[p + lo] = 1u;
+    }
+    __syncthreads();
+    const int G = (int)D + npen;
+
+    // 6. the tail's sums, on wave 0
+    if (wid == 0) {
+        const float *gval = L.u.g.gval;
+        const uint32_t *gcnt = L.u.g.gcnt;
+        const uint64_t n = (uint64_t)P.n;  // the reference's candidate count (V)
+        uint64_t in_list = 0;              // entries in the group list
+        for (int g = lane; g < G; g += 64) in_list += gcnt[g];
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) in_list += (uint64_t)__shfl_xor((unsigned long long)in_list, o);
+        auto eterm = [&](float x) { return zexpf_nb(x - mx); };
+        int sg = 0;
+        int64_t sc = 0;
+        uint64_t keep = n;
+        if (P.top_p < 1.0f) {  // :215-227
+            float total = 0.0f;
+            walk_groups(gval, gcnt, G, ~0ull, eterm, kWalkSum, 0.0f, total, &sg, &sc);
+            const float thr = P.top_p * total;
+            float acc = 0.0f;
+            const int64_t pos = walk_groups(gval, gcnt, G, ~0ull, eterm, kWalkReach, thr, acc, &sg, &sc);
+            keep = pos >= 0 ? (uint64_t)pos + 1 : n;
+        }
+        if (P.min_p > 0.0f) {  // :228-234: the first term below min_p within keep
+            uint64_t cum = 0, first = in_list;  // past the list every term is below min_p
+            for (int g0 = 0; g0 < G && cum < keep; g0 += 64) {
+                const int g = g0 + lane;
+                const uint32_t c = g < G ? gcnt[g] : 0u;
+                uint32_t cin = c;
+#pragma unroll
+                for (int o = 1; o < 64; o <<= 1) {
+                    const uint32_t y = __shfl_up(cin, o);
+                    if (lane >= o) cin += y;
+                }
+                const bool low = g < G && c > 0 && eterm(gval[g]) < P.min_p;
+                const uint64_t b = ballot(low);
+                if (b) {
+                    const int l = __ffsll((unsigned long long)b) - 1;
+                    first = cum + (uint32_t)__builtin_amdgcn_readlane(cin - c, l);
+                    break;
+                }
+                cum += (uint32_t)__builtin_amdgcn_readlane(cin, 63);
+            }
+            if (first < keep) keep = first > 1 ? first : 1;
+        }
+        if (keep > in_list) keep = in_list;  // more only with NaN logits, outside the reference's contract
+        // :236-242 temperature weights and their total over keep, then the draw (:270-275)
+        const float inv_t = 1.0f / P.temp;
+        auto wterm = [&](float x) { return zexpf_nb((x - mx) * inv_t); };
+        float total = 0.0f;
+        walk_groups(gval, gcnt, G, keep, wterm, kWalkSum, 0.0f, total, &sg, &sc);
+        const float u0 = P.uniforms[2 * row];
+        float r = u0 * total;
+        int64_t pick = walk_groups(gval, gcnt, G, keep, wterm, kWalkDrop, 0.0f, r, &sg, &sc);
+        if (pick < 0) {  // the last kept entry: its group and copy
+            pick = (int64_t)keep - 1;
+            uint64_t cum = 0;
+            sg = 0;
+            for (int g = 0; g < G; ++g) {
+                if (cum + gcnt[g] > (uint64_t)pick) {
+                    sg = g;
+                    break;
+                }
+                cum += gcnt[g];
+            }
+            sc = pick - (int64_t)cum;
+        }
+        // the entry's index among all entries of its value (equal groups are adjacent)
+        const float vt = gval[sg];
+        int64_t idx = sc;
+        for (int g = sg - 1; g >= 0 && gval[g] == vt; --g) idx += gcnt[g];
+        if (lane == 0) {
+            L.f[0] = vt;
+            L.i64[0] = idx;
+            L.i64[1] = (int64_t)keep;
+        }
+    }
+    __syncthreads();
+
+    // 7. the drawn entry's id: the (idx+1)-th entry of value vt in id order
+    const float vt = L.f[0];
+    const int64_t idx = L.i64[0];
+    const int64_t keep = L.i64[1];
+    int64_t seen = 0;
+    for (int t0 = 0; t0 < nvec; t0 += kThreads) {
+        const int q = t0 + tid;
+        uint32_t hit = 0u;  // entries of value vt in this thread's vector
+        if (q < nvec) {
+            const uint4 raw = *reinterpret_cast<const uint4 *>(lrow + q * VEC);
+            float v[VEC];
+            unpack<uint16_t>(raw, v);
+            const int id0 = q * VEC;
+            const uint32_t mb = HAS_MASK ? mrow[id0 >> 5] >> (id0 & 31) : 0xFFu;
+            const uint32_t pb = HAS_PEN ? (L.pbits[id0 >> 5] >> (id0 & 31)) : 0u;
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) {
+                if (id0 + e >= V) continue;
+                float x = v[e];
+                if (HAS_MASK && !((mb >> e) & 1u)) x = -INFINITY;
+                if ((pb >> e) & 1u) {  // a penalized entry: its value from the list
+                    x = __builtin_nanf("");
+                    for (int p = 0; p < npen; ++p)
+                        if (L.sid[p] == (uint32_t)(id0 + e)) x = L.sval[p];
+                }
+                if (x == vt) hit |= 1u << e;
+            }
+        }
+        const uint32_t c = (uint32_t)__popc(hit);
+        uint32_t cin = c;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t y = __shfl_up(cin, o);
+            if (lane >= o) cin += y;
+        }
+        if (lane == 63) L.wsum[wid] = cin;
+        __syncthreads();
+        uint32_t before = cin - c;
+        uint32_t tot = 0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            if (w < wid) before += L.wsum[w];
+            tot += L.wsum[w];
+        }
+        const int64_t lo = seen + before;
+        if (c && idx >= lo && idx < lo + c) {  // this thread holds it
+            uint32_t h = hit;
+            for (int64_t k = lo; k < idx; ++k) h &= h - 1u;
+            L.tok = (uint32_t)(q * VEC + __ffs(h) - 1);
+            L.found = 1;
+        }
+        seen += tot;
+        __syncthreads();
+        if (L.found) break;
+        __syncthreads();  // wsum is rewritten by the next tile
+    }
+    if (tid == 0) {
+        P.tok[row] = L.found ? L.tok : 0u;
+        P.margin[row] = (P.n >= 2) ? mx - second : 10.0f;
+        if (P.ndraws) P.ndraws[row] = 1;
+        if (P.keep) P.keep[row] = (int32_t)keep;
+        if (L.found) P.flags[row] = 0;  // settled here: the sorting pass skips it
+    }
+}
+
+template <bool M, bool PN>
+static hipError_t launch_whole_t(const ExactParams &P, int rows, hipStream_t st) {
+    hipLaunchKernelGGL((whole_kernel<M, PN>), dim3(rows), dim3(kThreads), 0, st, P);
+    return hipGetLastError();
+}
+
+hipError_t launch_whole(const ExactParams &P, int rows, hipStream_t st) {
+    const bool m = P.src.mask != nullptr;
+    const bool p = (P.src.hist != nullptr) || (P.src.edit_ids != nullptr);
+    if (m && p) return launch_whole_t<true, true>(P, rows, st);
+    if (m) return launch_whole_t<true, false>(P, rows, st);
+    if (p) return launch_whole_t<false, true>(P, rows, st);
+    return launch_whole_t<false, false>(P, rows, st);
+}
+
+}  // namespace zi
