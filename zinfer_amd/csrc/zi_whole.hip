@@ -36,6 +36,7 @@ namespace zi {
 constexpr int kWholeKeys = 4096;                   // distinct bf16 values above the floor
 constexpr int kWholePen = kOwnSlots * kThreads;    // penalized entries (window + edits), one per owner slot
 constexpr int kWholeGroups = kWholeKeys + kWholePen;
+constexpr int kWholeBatch = 4;  // row vectors in flight per thread
 
 struct WholeLds {
     uint32_t pbits[kMaxVocab / 32];  // penalized ids
@@ -50,16 +51,22 @@ struct WholeLds {
             uint32_t gcnt[kWholeGroups];
         } g;
     } u;
-    uint32_t kbits[65536 / 32];  // present keys
-    uint32_t wsuf[65536 / 32];   // present keys (at or above the floor) in words above each word
-    uint32_t bcnt[kWholeKeys];   // entries per key rank
-    uint16_t bkey[kWholeKeys];   // key of each rank
+    union {
+        struct {                         // steps 2-5
+            uint32_t kbits[65536 / 32];  // present keys
+            uint32_t wsuf[65536 / 32];   // present keys (at or above the floor) in words above each word
+            uint32_t bcnt[kWholeKeys];   // entries per key rank
+            uint16_t bkey[kWholeKeys];   // key of each rank
+        } k;
+        uint32_t vbits[kMaxVocab / 32];  // step 7: penalized ids whose value is the drawn one
+    } w;
     float pval[kWholePen];       // penalized entries: value, id (then sorted by value desc, id asc)
     uint32_t pid[kWholePen];
     float sval[kWholePen];
     uint32_t sid[kWholePen];
     float wt1[kWaves], wt2[kWaves];
     uint32_t wsum[kWaves];
+    uint32_t tcnt[kMaxVocab / (8 * kThreads)];  // entries of the drawn value per 4096-id tile
     int npen, nsel;
     int found;
     uint32_t tok;
@@ -237,7 +244,7 @@ __global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
         for (int s = 0; s < kOwnSlots; ++s)
             if (oid[s] != 0xFFFFFFFFu) oraw[s] = (uint32_t)lrow[oid[s]];
     }
-    for (int i = tid; i < 65536 / 32; i += kThreads) L.kbits[i] = 0u;
+    for (int i = tid; i < 65536 / 32; i += kThreads) L.w.k.kbits[i] = 0u;
     if (tid == 0) {
         L.npen = 0;
         L.nsel = 0;
@@ -247,23 +254,39 @@ __global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
 
     // 2. row max / second (unpenalized entries), present keys
     float t1 = -INFINITY, t2 = -INFINITY;
-    for (int q = tid; q < nvec; q += kThreads) {
-        const uint4 raw = *reinterpret_cast<const uint4 *>(lrow + q * VEC);
-        float v[VEC];
-        unpack<uint16_t>(raw, v);
-        const int id0 = q * VEC;
-        const uint32_t mb = HAS_MASK ? mrow[id0 >> 5] >> (id0 & 31) : 0xFFu;
-        const uint32_t pb = HAS_PEN ? (L.pbits[id0 >> 5] >> (id0 & 31)) : 0u;
+    for (int q0 = tid; q0 < nvec; q0 += kThreads * kWholeBatch) {
+        uint4 rawb[kWholeBatch];
+        uint32_t mwb[kWholeBatch];
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-            if (id0 + e >= V || ((pb >> e) & 1u)) continue;
-            float x = v[e];
-            if (HAS_MASK && !((mb >> e) & 1u)) x = -INFINITY;
-            if (x != x) continue;  // NaN: no place in the order (outside the reference's contract)
-            top2_merge(t1, t2, x);
-            const uint32_t k = key16(x);
-            const uint32_t bit = 1u << (k & 31);
-            if (!(L.kbits[k >> 5] & bit)) atomicOr(&L.kbits[k >> 5], bit);
+        for (int j = 0; j < kWholeBatch; ++j) {  // every load first
+            const int q = q0 + j * kThreads;
+            rawb[j] = make_uint4(0u, 0u, 0u, 0u);
+            mwb[j] = 0u;
+            if (q < nvec) {
+                rawb[j] = *reinterpret_cast<const uint4 *>(lrow + q * VEC);
+                if (HAS_MASK) mwb[j] = mrow[(q * VEC) >> 5];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < kWholeBatch; ++j) {
+            const int q = q0 + j * kThreads;
+            if (q >= nvec) break;
+            float v[VEC];
+            unpack<uint16_t>(rawb[j], v);
+            const int id0 = q * VEC;
+            const uint32_t mb = HAS_MASK ? mwb[j] >> (id0 & 31) : 0xFFu;
+            const uint32_t pb = HAS_PEN ? (L.pbits[id0 >> 5] >> (id0 & 31)) : 0u;
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) {
+                if (id0 + e >= V || ((pb >> e) & 1u)) continue;
+                float x = v[e];
+                if (HAS_MASK && !((mb >> e) & 1u)) x = -INFINITY;
+                if (x != x) continue;  // NaN: no place in the order (outside the reference's contract)
+                top2_merge(t1, t2, x);
+                const uint32_t k = key16(x);
+                const uint32_t bit = 1u << (k & 31);
+                if (!(L.w.k.kbits[k >> 5] & bit)) atomicOr(&L.w.k.kbits[k >> 5], bit);
+            }
         }
     }
     // 3. penalized values
@@ -317,10 +340,10 @@ __global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const uint32_t w = (uint32_t)(4 * tid + j);
-        uint32_t bits = L.kbits[w];
+        uint32_t bits = L.w.k.kbits[w];
         if (w * 32 + 31 < kmin) bits = 0u;
         else if (w * 32 < kmin) bits &= ~0u << (kmin - w * 32);
-        L.kbits[w] = bits;
+        L.w.k.kbits[w] = bits;
         wc[j] = (uint32_t)__popc(bits);
         mine += wc[j];
     }
@@ -345,13 +368,13 @@ __global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
 #pragma unroll
     for (int j = 3; j >= 0; --j) {  // words in descending order within this thread
         const uint32_t w = (uint32_t)(4 * tid + j);
-        L.wsuf[w] = above;
-        uint32_t bits = L.kbits[w];
+        L.w.k.wsuf[w] = above;
+        uint32_t bits = L.w.k.kbits[w];
         uint32_t r = above;
         while (bits) {  // highest key first
             const int b = 31 - __clz(bits);
-            L.bkey[r] = (uint16_t)(w * 32 + (uint32_t)b);
-            L.bcnt[r] = 0u;
+            L.w.k.bkey[r] = (uint16_t)(w * 32 + (uint32_t)b);
+            L.w.k.bcnt[r] = 0u;
             ++r;
             bits &= ~(1u << b);
         }
@@ -360,23 +383,39 @@ __global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
     __syncthreads();
 
     // 4. counts per key rank
-    for (int q = tid; q < nvec; q += kThreads) {
-        const uint4 raw = *reinterpret_cast<const uint4 *>(lrow + q * VEC);
-        float v[VEC];
-        unpack<uint16_t>(raw, v);
-        const int id0 = q * VEC;
-        const uint32_t mb = HAS_MASK ? mrow[id0 >> 5] >> (id0 & 31) : 0xFFu;
-        const uint32_t pb = HAS_PEN ? (L.pbits[id0 >> 5] >> (id0 & 31)) : 0u;
+    for (int q0 = tid; q0 < nvec; q0 += kThreads * kWholeBatch) {
+        uint4 rawb[kWholeBatch];
+        uint32_t mwb[kWholeBatch];
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-            if (id0 + e >= V || ((pb >> e) & 1u)) continue;
-            float x = v[e];
-            if (HAS_MASK && !((mb >> e) & 1u)) x = -INFINITY;
-            if (x != x) continue;
-            const uint32_t k = key16(x);
-            if (k < kmin) continue;
-            const uint32_t w = k >> 5, above_in = L.kbits[w] >> (k & 31) >> 1;
-            atomicAdd(&L.bcnt[L.wsuf[w] + (uint32_t)__popc(above_in)], 1u);
+        for (int j = 0; j < kWholeBatch; ++j) {  // every load first
+            const int q = q0 + j * kThreads;
+            rawb[j] = make_uint4(0u, 0u, 0u, 0u);
+            mwb[j] = 0u;
+            if (q < nvec) {
+                rawb[j] = *reinterpret_cast<const uint4 *>(lrow + q * VEC);
+                if (HAS_MASK) mwb[j] = mrow[(q * VEC) >> 5];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < kWholeBatch; ++j) {
+            const int q = q0 + j * kThreads;
+            if (q >= nvec) break;
+            float v[VEC];
+            unpack<uint16_t>(rawb[j], v);
+            const int id0 = q * VEC;
+            const uint32_t mb = HAS_MASK ? mwb[j] >> (id0 & 31) : 0xFFu;
+            const uint32_t pb = HAS_PEN ? (L.pbits[id0 >> 5] >> (id0 & 31)) : 0u;
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) {
+                if (id0 + e >= V || ((pb >> e) & 1u)) continue;
+                float x = v[e];
+                if (HAS_MASK && !((mb >> e) & 1u)) x = -INFINITY;
+                if (x != x) continue;
+                const uint32_t k = key16(x);
+                if (k < kmin) continue;
+                const uint32_t w = k >> 5, above_in = L.w.k.kbits[w] >> (k & 31) >> 1;
+                atomicAdd(&L.w.k.bcnt[L.w.k.wsuf[w] + (uint32_t)__popc(above_in)], 1u);
+            }
         }
     }
     // penalized entries ranked by (value desc, id asc)
@@ -396,7 +435,7 @@ __global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
     // 5. the group list, key groups and penalized entries merged by value
     //    (a key group before the penalized entries of its value)
     for (int r = tid; r < (int)D; r += kThreads) {
-        const float vr = key16_value(L.bkey[r]);
+        const float vr = key16_value(L.w.k.bkey[r]);
         int lo = 0, hi = npen;  // penalized entries with value > vr
         while (lo < hi) {
             const int mid = (lo + hi) >> 1;
@@ -404,14 +443,14 @@ __global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
             else hi = mid;
         }
         L.u.g.gval[r + lo] = vr;
-        L.u.g.gcnt[r + lo] = L.bcnt[r];
+        L.u.g.gcnt[r + lo] = L.w.k.bcnt[r];
     }
     for (int p = tid; p < npen; p += kThreads) {
         const float vp = L.sval[p];
         int lo = 0, hi = (int)D;  // key groups with value >= vp
         while (lo < hi) {
             const int mid = (lo + hi) >> 1;
-            if (key16_value(L.bkey[mid]) >= vp) lo = mid + 1;
+            if (key16_value(L.w.k.bkey[mid]) >= vp) lo = mid + 1;
             else hi = mid;
         }
         L.u.g.gval[p + lo] = vp;
@@ -497,34 +536,75 @@ __global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
     }
     __syncthreads();
 
-    // 7. the drawn entry's id: the (idx+1)-th entry of value vt in id order
+    // 7. the drawn entry's id: the (idx+1)-th entry of value vt in id order.
+    //    One read of the row counts each 4096-id tile's entries of value vt
+    //    (kWholeBatch vectors in flight per thread); the tile that holds the
+    //    entry is read again and ranked.
     const float vt = L.f[0];
     const int64_t idx = L.i64[0];
     const int64_t keep = L.i64[1];
-    int64_t seen = 0;
-    for (int t0 = 0; t0 < nvec; t0 += kThreads) {
-        const int q = t0 + tid;
-        uint32_t hit = 0u;  // entries of value vt in this thread's vector
-        if (q < nvec) {
-            const uint4 raw = *reinterpret_cast<const uint4 *>(lrow + q * VEC);
-            float v[VEC];
-            unpack<uint16_t>(raw, v);
-            const int id0 = q * VEC;
-            const uint32_t mb = HAS_MASK ? mrow[id0 >> 5] >> (id0 & 31) : 0xFFu;
-            const uint32_t pb = HAS_PEN ? (L.pbits[id0 >> 5] >> (id0 & 31)) : 0u;
+    const int ntile = (nvec + kThreads - 1) / kThreads;
+    auto vhit = [&](const uint4 &raw, uint32_t mword, int q) -> uint32_t {  // entries of value vt in vector q
+        float v[VEC];
+        unpack<uint16_t>(raw, v);
+        const int id0 = q * VEC;
+        const uint32_t mb = HAS_MASK ? mword >> (id0 & 31) : 0xFFu;
+        const uint32_t pb = HAS_PEN ? (L.pbits[id0 >> 5] >> (id0 & 31)) : 0u;
+        uint32_t hit = 0u;
 #pragma unroll
-            for (int e = 0; e < VEC; ++e) {
-                if (id0 + e >= V) continue;
-                float x = v[e];
-                if (HAS_MASK && !((mb >> e) & 1u)) x = -INFINITY;
-                if ((pb >> e) & 1u) {  // a penalized entry: its value from the list
-                    x = __builtin_nanf("");
-                    for (int p = 0; p < npen; ++p)
-                        if (L.sid[p] == (uint32_t)(id0 + e)) x = L.sval[p];
-                }
-                if (x == vt) hit |= 1u << e;
+        for (int e = 0; e < VEC; ++e) {
+            if (id0 + e >= V) continue;
+            float x = v[e];
+            if (HAS_MASK && !((mb >> e) & 1u)) x = -INFINITY;
+            if (!((pb >> e) & 1u) && x == vt) hit |= 1u << e;
+        }
+        if (HAS_PEN) hit |= (L.w.vbits[id0 >> 5] >> (id0 & 31)) & 0xFFu;  // penalized ones of value vt
+        return hit;
+    };
+    for (int i = tid; i < ntile; i += kThreads) L.tcnt[i] = 0u;
+    if (HAS_PEN) {
+        for (int i = tid; i < (V + 31) / 32; i += kThreads) L.w.vbits[i] = 0u;
+        __syncthreads();
+        for (int p = tid; p < npen; p += kThreads)
+            if (L.sval[p] == vt) atomicOr(&L.w.vbits[L.sid[p] >> 5], 1u << (L.sid[p] & 31));
+    }
+    __syncthreads();
+    for (int t0 = 0; t0 < ntile; t0 += kWholeBatch) {
+        uint4 raw[kWholeBatch];
+        uint32_t mw[kWholeBatch];
+#pragma unroll
+        for (int j = 0; j < kWholeBatch; ++j) {  // every load first
+            const int q = (t0 + j) * kThreads + tid;
+            raw[j] = make_uint4(0u, 0u, 0u, 0u);
+            mw[j] = 0u;
+            if (q < nvec) {
+                raw[j] = *reinterpret_cast<const uint4 *>(lrow + q * VEC);
+                if (HAS_MASK) mw[j] = mrow[(q * VEC) >> 5];
             }
         }
+#pragma unroll
+        for (int j = 0; j < kWholeBatch; ++j) {
+            const int q = (t0 + j) * kThreads + tid;
+            uint32_t c = q < nvec ? (uint32_t)__popc(vhit(raw[j], mw[j], q)) : 0u;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) c += __shfl_xor(c, o);
+            if (lane == 0 && c) atomicAdd(&L.tcnt[t0 + j], c);
+        }
+    }
+    __syncthreads();
+    int tj = -1;
+    int64_t seen = 0;  // entries of value vt in the tiles before tj
+    for (int j = 0; j < ntile; ++j) {
+        if (seen + (int64_t)L.tcnt[j] > idx) {
+            tj = j;
+            break;
+        }
+        seen += L.tcnt[j];
+    }
+    if (tj >= 0) {  // uniform
+        const int q = tj * kThreads + tid;
+        uint32_t hit = 0u;
+        if (q < nvec) hit = vhit(*reinterpret_cast<const uint4 *>(lrow + q * VEC), HAS_MASK ? mrow[(q * VEC) >> 5] : 0u, q);
         const uint32_t c = (uint32_t)__popc(hit);
         uint32_t cin = c;
 #pragma unroll
@@ -535,12 +615,9 @@ __global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
         if (lane == 63) L.wsum[wid] = cin;
         __syncthreads();
         uint32_t before = cin - c;
-        uint32_t tot = 0;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
+        for (int w = 0; w < kWaves; ++w)
             if (w < wid) before += L.wsum[w];
-            tot += L.wsum[w];
-        }
         const int64_t lo = seen + before;
         if (c && idx >= lo && idx < lo + c) {  // this thread holds it
             uint32_t h = hit;
@@ -548,11 +625,8 @@ __global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
             L.tok = (uint32_t)(q * VEC + __ffs(h) - 1);
             L.found = 1;
         }
-        seen += tot;
-        __syncthreads();
-        if (L.found) break;
-        __syncthreads();  // wsum is rewritten by the next tile
     }
+    __syncthreads();
     if (tid == 0) {
         P.tok[row] = L.found ? L.tok : 0u;
         P.margin[row] = (P.n >= 2) ? mx - second : 10.0f;
