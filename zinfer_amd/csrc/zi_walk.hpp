@@ -74,8 +74,11 @@ __host__ __device__ inline WalkTerm walk_term(float t, int qe) {
     return w;
 }
 __host__ __device__ inline uint64_t walk_sat(uint64_t a) { return a > kWalkSat ? kWalkSat : a; }
-__host__ __device__ inline uint64_t walk_mul(uint64_t c, uint64_t d) {  // min(c d, kWalkSat), no overflow
-    return (d != 0 && c > kWalkSat / d) ? kWalkSat : walk_sat(c * d);
+// min(c d, kWalkSat) without overflow or an integer division: a product the
+// double estimate puts at or above kWalkSat saturates (anything above 2^25
+// only ever signals that the grid is left, so the exact cut does not matter).
+__host__ __device__ inline uint64_t walk_mul(uint64_t c, uint64_t d) {
+    return (double)c * (double)d >= (double)kWalkSat ? kWalkSat : c * d;
 }
 
 // c copies of one term as a map of m's parity p: increment inc[p], parity out.

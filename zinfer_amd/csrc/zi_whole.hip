@@ -36,7 +36,7 @@ namespace zi {
 constexpr int kWholeKeys = 4096;                   // distinct bf16 values above the floor
 constexpr int kWholePen = kOwnSlots * kThreads;    // penalized entries (window + edits), one per owner slot
 constexpr int kWholeGroups = kWholeKeys + kWholePen;
-constexpr int kWholeBatch = 4;  // row vectors in flight per thread
+constexpr int kWholeBatch = 16;  // row vectors in flight per thread
 
 struct WholeLds {
     uint32_t pbits[kMaxVocab / 32];  // penalized ids
@@ -59,7 +59,17 @@ struct WholeLds {
             uint16_t bkey[kWholeKeys];   // key of each rank
         } k;
         uint32_t vbits[kMaxVocab / 32];  // step 7: penalized ids whose value is the drawn one
+        uint32_t gpos[kWholeGroups];     // step 6: entries before each group
     } w;
+    struct {  // block walks: the waves' total maps and first events, by chunk parity
+        uint64_t inc0[2][kWaves], inc1[2][kWaves];
+        uint32_t par[2][kWaves];
+        int ev[2][kWaves];
+        uint64_t ep;
+        float et;
+        uint32_t ec;
+        int first;
+    } wb;
     float pval[kWholePen];       // penalized entries: value, id (then sorted by value desc, id asc)
     uint32_t pid[kWholePen];
     float sval[kWholePen];
@@ -107,8 +117,12 @@ __device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l) {
 }
 
 // One wave walks groups [0, G) over their first `limit` entries (every lane
-// active, uniform result).  Returns the entry index at which the walk stops
-// (group *sg, copy *sc), or -1; v is the running value.
+// active, uniform result), kWalkPer consecutive groups per lane: each lane
+// composes its groups' maps, the wave scans the lanes' maps, and the lane with
+// the first event walks its own groups to place it.  Returns the entry index
+// at which the walk stops (group *sg, copy *sc), or -1; v is the running value.
+constexpr int kWalkPer = 1;
+
 template <class Term>
 __device__ int64_t walk_groups(const float *gval, const uint32_t *gcnt, int G, uint64_t limit, Term term, int mode,
                                float thr, float &v, int *sg, int64_t *sc) {
@@ -130,20 +144,36 @@ __device__ int64_t walk_groups(const float *gval, const uint32_t *gcnt, int G, u
         }
         const WalkGrid gr = walk_grid(v);
         const uint32_t p0 = gr.m & 1u;
-        const int gl = g + lane;
-        const uint32_t craw = gl < G ? gcnt[gl] : 0u;
-        uint32_t cin = craw;  // inclusive prefix of the raw counts
+        const int gb = g + lane * kWalkPer;
+        uint32_t craw[kWalkPer], lraw = 0;
+#pragma unroll
+        for (int k = 0; k < kWalkPer; ++k) {
+            craw[k] = gb + k < G ? gcnt[gb + k] : 0u;
+            lraw += craw[k];
+        }
+        uint32_t rin = lraw;  // inclusive prefix of the lanes' raw counts
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
-            const uint32_t y = __shfl_up(cin, o);
-            if (lane >= o) cin += y;
+            const uint32_t y = __shfl_up(rin, o);
+            if (lane >= o) rin += y;
         }
-        const uint64_t before = cum + (cin - craw);
-        const uint32_t c = before >= limit ? 0u : (uint32_t)min_u64((uint64_t)craw, limit - before);
-        const float t = c ? term(gval[gl]) : 0.0f;
-        WalkMap mp = walk_map(walk_term(t, gr.qe), c);
+        uint64_t before = cum + (rin - lraw);
+        uint32_t c[kWalkPer], lc = 0;
+        float t[kWalkPer];
+        WalkMap mk[kWalkPer];
+#pragma unroll
+        for (int k = 0; k < kWalkPer; ++k) {  // counts clamped at limit, terms, maps
+            c[k] = before >= limit ? 0u : (uint32_t)min_u64((uint64_t)craw[k], limit - before);
+            before += craw[k];
+            lc += c[k];
+            t[k] = c[k] ? term(gval[gb + k]) : 0.0f;
+            mk[k] = walk_map(walk_term(t[k], gr.qe), c[k]);
+        }
+        WalkMap mp = mk[0];
+#pragma unroll
+        for (int k = 1; k < kWalkPer; ++k) mp = walk_compose(mp, mk[k]);
         uint32_t par = mp.par0 | (mp.par1 << 1);
-        uint32_t ccl = c;  // inclusive prefix of the clamped counts
+        uint32_t ccl = lc;  // inclusive prefix of the lanes' clamped counts
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {  // inclusive scan: earlier lanes' map, then this lane's
             WalkMap pm;
@@ -159,31 +189,182 @@ __device__ int64_t walk_groups(const float *gval, const uint32_t *gcnt, int G, u
                 ccl += yc;
             }
         }
-        const uint64_t P = p0 ? mp.inc1 : mp.inc0;
-        const bool ev = c > 0 && walk_event(gr.m, gr.qe, P, mode, thr);
-        const uint64_t b = ballot(ev);
+        // the lanes before this one: their inclusive map and count
+        WalkMap run;
+        run.inc0 = shfl_up_u64(mp.inc0, 1);
+        run.inc1 = shfl_up_u64(mp.inc1, 1);
+        const uint32_t pp = __shfl_up(par, 1);
+        run.par0 = pp & 1u;
+        run.par1 = pp >> 1;
+        uint32_t cex = __shfl_up(ccl, 1);
+        if (lane == 0) {
+            run.inc0 = run.inc1 = 0;
+            run.par0 = 0;
+            run.par1 = 1;
+            cex = 0;
+        }
+        // this lane's first event, if any: its group, the prefix before it
+        int ek = -1;
+        uint64_t pb = 0;
+        uint32_t cb = 0, ce = 0;
+        float te = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kWalkPer; ++k) {
+            const WalkMap nx = walk_compose(run, mk[k]);
+            const uint64_t P = p0 ? nx.inc1 : nx.inc0;
+            if (ek < 0 && c[k] > 0 && walk_event(gr.m, gr.qe, P, mode, thr)) {
+                ek = k;
+                pb = p0 ? run.inc1 : run.inc0;
+                cb = cex;
+                ce = c[k];
+                te = t[k];
+            }
+            cex += c[k];
+            run = nx;
+        }
+        const uint64_t b = ballot(ek >= 0);
         if (!b) {
-            const uint64_t P63 = readlane_u64(P, 63);
+            const uint64_t P63 = readlane_u64(p0 ? mp.inc1 : mp.inc0, 63);
             v = walk_value(mode == kWalkDrop ? gr.m - P63 : gr.m + P63, gr.qe);
             cum += (uint32_t)__builtin_amdgcn_readlane(ccl, 63);
-            g += 64;
+            g += 64 * kWalkPer;
             continue;
         }
         const int L = __ffsll((unsigned long long)b) - 1;
-        const uint64_t Pp = L > 0 ? readlane_u64(P, L - 1) : 0;
-        const uint32_t cp = L > 0 ? (uint32_t)__builtin_amdgcn_readlane(ccl, L - 1) : 0u;
+        const uint64_t Pp = readlane_u64(pb, L);
         v = walk_value(mode == kWalkDrop ? gr.m - Pp : gr.m + Pp, gr.qe);
-        cum += cp;
-        const float tL = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), L));
-        const uint32_t cL = (uint32_t)__builtin_amdgcn_readlane(c, L);
-        const int64_t s = walk_group(v, tL, cL, mode, thr);
-        if (s >= 0) {
-            *sg = g + L;
-            *sc = s;
-            return (int64_t)cum + s;
+        cum += (uint32_t)__builtin_amdgcn_readlane(cb, L);
+        const int gE = g + L * kWalkPer + __builtin_amdgcn_readlane(ek, L);
+        const float tL = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(te), L));
+        const uint32_t cL = (uint32_t)__builtin_amdgcn_readlane(ce, L);
+        const int64_t s2 = walk_group(v, tL, cL, mode, thr);
+        if (s2 >= 0) {
+            *sg = gE;
+            *sc = s2;
+            return (int64_t)cum + s2;
         }
         cum += cL;
-        g += L + 1;
+        g = gE + 1;
+    }
+    return -1;
+}
+
+// The whole workgroup walks groups [0, gk], the last of them over its first
+// ck entries: a chunk of 512 groups per step, one per thread, the maps scanned
+// over the wave and then across the waves; only the group of the first event
+// is walked on its own (by every thread alike).  Every thread calls it and
+// gets the same result: the entry index at which the walk stops (group *sg,
+// copy *sc), or -1; v is the running value.
+template <class Term, class WB>
+__device__ int64_t walk_block(const float *gval, const uint32_t *gcnt, const uint32_t *gpos, int gk, uint32_t ck,
+                              Term term, int mode, float thr, float &v, int *sg, int64_t *sc, WB &W) {
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    int g = 0, buf = 0;
+    while (g <= gk) {
+        if ((mode != kWalkDrop && v == 0.0f) || (mode == kWalkDrop && !(v > 0.0f))) {  // no grid yet: one group
+            const int64_t s = walk_group(v, term(gval[g]), g == gk ? ck : gcnt[g], mode, thr);
+            if (s >= 0) {
+                *sg = g;
+                *sc = s;
+                return (int64_t)gpos[g] + s;
+            }
+            ++g;
+            continue;
+        }
+        const WalkGrid gr = walk_grid(v);
+        const uint32_t p0 = gr.m & 1u;
+        const int gl = g + tid;
+        const uint32_t c = gl < gk ? gcnt[gl] : (gl == gk ? ck : 0u);
+        const float t = c ? term(gval[gl]) : 0.0f;
+        WalkMap mp = walk_map(walk_term(t, gr.qe), c);
+        uint32_t par = mp.par0 | (mp.par1 << 1);
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {  // inclusive over the wave: earlier lanes' map, then this lane's
+            WalkMap pm;
+            pm.inc0 = shfl_up_u64(mp.inc0, o);
+            pm.inc1 = shfl_up_u64(mp.inc1, o);
+            const uint32_t pp = __shfl_up(par, o);
+            pm.par0 = pp & 1u;
+            pm.par1 = pp >> 1;
+            if (lane >= o) {
+                mp = walk_compose(pm, mp);
+                par = mp.par0 | (mp.par1 << 1);
+            }
+        }
+        WalkMap ex;  // the wave's lanes before this one
+        ex.inc0 = shfl_up_u64(mp.inc0, 1);
+        ex.inc1 = shfl_up_u64(mp.inc1, 1);
+        const uint32_t pe = __shfl_up(par, 1);
+        ex.par0 = pe & 1u;
+        ex.par1 = pe >> 1;
+        if (lane == 0) {
+            ex.inc0 = ex.inc1 = 0;
+            ex.par0 = 0;
+            ex.par1 = 1;
+        }
+        if (lane == 63) {
+            W.inc0[buf][wid] = mp.inc0;
+            W.inc1[buf][wid] = mp.inc1;
+            W.par[buf][wid] = par;
+        }
+        __syncthreads();
+        WalkMap pre;  // the waves before this one
+        pre.inc0 = pre.inc1 = 0;
+        pre.par0 = 0;
+        pre.par1 = 1;
+        for (int w = 0; w < wid; ++w) {
+            WalkMap o;
+            o.inc0 = W.inc0[buf][w];
+            o.inc1 = W.inc1[buf][w];
+            o.par0 = W.par[buf][w] & 1u;
+            o.par1 = W.par[buf][w] >> 1;
+            pre = walk_compose(pre, o);
+        }
+        const WalkMap in = walk_compose(pre, mp);
+        const bool ev = c > 0 && walk_event(gr.m, gr.qe, p0 ? in.inc1 : in.inc0, mode, thr);
+        const uint64_t b = ballot(ev);
+        if (lane == 0) W.ev[buf][wid] = b ? __ffsll((unsigned long long)b) - 1 : 64;
+        __syncthreads();
+        int E = -1;
+        for (int w = 0; w < kWaves && E < 0; ++w)
+            if (W.ev[buf][w] < 64) E = w * 64 + W.ev[buf][w];
+        if (E < 0) {  // no event in the chunk: all of it as integers
+            WalkMap tot = pre;
+            for (int w = wid; w < kWaves; ++w) {
+                WalkMap o;
+                o.inc0 = W.inc0[buf][w];
+                o.inc1 = W.inc1[buf][w];
+                o.par0 = W.par[buf][w] & 1u;
+                o.par1 = W.par[buf][w] >> 1;
+                tot = walk_compose(tot, o);
+            }
+            const uint64_t Pt = p0 ? tot.inc1 : tot.inc0;
+            v = walk_value(mode == kWalkDrop ? gr.m - Pt : gr.m + Pt, gr.qe);
+            g += kThreads;
+            buf ^= 1;
+            continue;
+        }
+        if (tid == E) {
+            const WalkMap bx = walk_compose(pre, ex);
+            W.ep = p0 ? bx.inc1 : bx.inc0;
+            W.et = t;
+            W.ec = c;
+        }
+        __syncthreads();
+        const uint64_t Pp = W.ep;
+        const float te = W.et;
+        const uint32_t ce = W.ec;
+        __syncthreads();  // read by every thread before the next event rewrites them
+        v = walk_value(mode == kWalkDrop ? gr.m - Pp : gr.m + Pp, gr.qe);
+        const int64_t s = walk_group(v, te, ce, mode, thr);
+        const int ge = g + E;
+        if (s >= 0) {
+            *sg = ge;
+            *sc = s;
+            return (int64_t)gpos[ge] + s;
+        }
+        g = ge + 1;
+        buf ^= 1;
     }
     return -1;
 }
@@ -459,90 +640,93 @@ __global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
     __syncthreads();
     const int G = (int)D + npen;
 
-    // 6. the tail's sums, on wave 0
-    if (wid == 0) {
-        const float *gval = L.u.g.gval;
-        const uint32_t *gcnt = L.u.g.gcnt;
-        const uint64_t n = (uint64_t)P.n;  // the reference's candidate count (V)
-        uint64_t in_list = 0;              // entries in the group list
-        for (int g = lane; g < G; g += 64) in_list += gcnt[g];
+    // 6. the tail's sums, every thread walking alike; first the entries
+    //    before each group
+    {
+        constexpr int kPer = (kWholeGroups + kThreads - 1) / kThreads;
+        const int g0 = tid * kPer;
+        uint32_t loc = 0;
+        for (int k = 0; k < kPer; ++k)
+            if (g0 + k < G) loc += L.u.g.gcnt[g0 + k];
+        uint32_t incl = loc;
 #pragma unroll
-        for (int o = 1; o < 64; o <<= 1) in_list += (uint64_t)__shfl_xor((unsigned long long)in_list, o);
-        auto eterm = [&](float x) { return zexpf_nb(x - mx); };
-        int sg = 0;
-        int64_t sc = 0;
-        uint64_t keep = n;
-        if (P.top_p < 1.0f) {  // :215-227
-            float total = 0.0f;
-            walk_groups(gval, gcnt, G, ~0ull, eterm, kWalkSum, 0.0f, total, &sg, &sc);
-            const float thr = P.top_p * total;
-            float acc = 0.0f;
-            const int64_t pos = walk_groups(gval, gcnt, G, ~0ull, eterm, kWalkReach, thr, acc, &sg, &sc);
-            keep = pos >= 0 ? (uint64_t)pos + 1 : n;
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t y = __shfl_up(incl, o);
+            if (lane >= o) incl += y;
         }
-        if (P.min_p > 0.0f) {  // :228-234: the first term below min_p within keep
-            uint64_t cum = 0, first = in_list;  // past the list every term is below min_p
-            for (int g0 = 0; g0 < G && cum < keep; g0 += 64) {
-                const int g = g0 + lane;
-                const uint32_t c = g < G ? gcnt[g] : 0u;
-                uint32_t cin = c;
-#pragma unroll
-                for (int o = 1; o < 64; o <<= 1) {
-                    const uint32_t y = __shfl_up(cin, o);
-                    if (lane >= o) cin += y;
-                }
-                const bool low = g < G && c > 0 && eterm(gval[g]) < P.min_p;
-                const uint64_t b = ballot(low);
-                if (b) {
-                    const int l = __ffsll((unsigned long long)b) - 1;
-                    first = cum + (uint32_t)__builtin_amdgcn_readlane(cin - c, l);
-                    break;
-                }
-                cum += (uint32_t)__builtin_amdgcn_readlane(cin, 63);
+        if (lane == 63) L.wsum[wid] = incl;
+        __syncthreads();
+        uint32_t run = incl - loc;
+        for (int w = 0; w < wid; ++w) run += L.wsum[w];
+        for (int k = 0; k < kPer; ++k)
+            if (g0 + k < G) {
+                L.w.gpos[g0 + k] = run;
+                run += L.u.g.gcnt[g0 + k];
             }
-            if (first < keep) keep = first > 1 ? first : 1;
-        }
-        if (keep > in_list) keep = in_list;  // more only with NaN logits, outside the reference's contract
-        // :236-242 temperature weights and their total over keep, then the draw (:270-275)
-        const float inv_t = 1.0f / P.temp;
-        auto wterm = [&](float x) { return zexpf_nb((x - mx) * inv_t); };
-        float total = 0.0f;
-        walk_groups(gval, gcnt, G, keep, wterm, kWalkSum, 0.0f, total, &sg, &sc);
-        const float u0 = P.uniforms[2 * row];
-        float r = u0 * total;
-        int64_t pick = walk_groups(gval, gcnt, G, keep, wterm, kWalkDrop, 0.0f, r, &sg, &sc);
-        if (pick < 0) {  // the last kept entry: its group and copy
-            pick = (int64_t)keep - 1;
-            uint64_t cum = 0;
-            sg = 0;
-            for (int g = 0; g < G; ++g) {
-                if (cum + gcnt[g] > (uint64_t)pick) {
-                    sg = g;
-                    break;
-                }
-                cum += gcnt[g];
-            }
-            sc = pick - (int64_t)cum;
-        }
-        // the entry's index among all entries of its value (equal groups are adjacent)
-        const float vt = gval[sg];
-        int64_t idx = sc;
-        for (int g = sg - 1; g >= 0 && gval[g] == vt; --g) idx += gcnt[g];
-        if (lane == 0) {
-            L.f[0] = vt;
-            L.i64[0] = idx;
-            L.i64[1] = (int64_t)keep;
-        }
+        __syncthreads();
     }
-    __syncthreads();
+    const float *gval = L.u.g.gval;
+    const uint32_t *gcnt = L.u.g.gcnt;
+    const uint32_t *gpos = L.w.gpos;
+    const uint64_t in_list = (uint64_t)gpos[G - 1] + gcnt[G - 1];  // entries in the group list
+    // the group holding entry e - 1 and how many of its entries come before e
+    auto cut = [&](uint64_t e, int &gk, uint32_t &ck) {
+        int lo = 0, hi = G - 1;  // last group with gpos <= e - 1
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if ((uint64_t)gpos[mid] <= e - 1) lo = mid;
+            else hi = mid - 1;
+        }
+        gk = lo;
+        ck = (uint32_t)(e - gpos[lo]);
+    };
+    auto eterm = [&](float x) { return zexpf_nb(x - mx); };
+    int sg = 0;
+    int64_t sc = 0;
+    uint64_t keep = (uint64_t)P.n;  // the reference's candidate count (V)
+    if (P.top_p < 1.0f) {          // :215-227
+        float total = 0.0f;
+        walk_block(gval, gcnt, gpos, G - 1, gcnt[G - 1], eterm, kWalkSum, 0.0f, total, &sg, &sc, L.wb);
+        const float thr = P.top_p * total;
+        float acc = 0.0f;
+        const int64_t pos = walk_block(gval, gcnt, gpos, G - 1, gcnt[G - 1], eterm, kWalkReach, thr, acc, &sg, &sc, L.wb);
+        keep = pos >= 0 ? (uint64_t)pos + 1 : keep;
+    }
+    if (P.min_p > 0.0f) {  // :228-234: the first term below min_p within keep
+        if (tid == 0) L.wb.first = G;
+        __syncthreads();
+        for (int g = tid; g < G; g += kThreads)
+            if (gcnt[g] > 0 && (uint64_t)gpos[g] < keep && eterm(gval[g]) < P.min_p) atomicMin(&L.wb.first, g);
+        __syncthreads();
+        const int fg = L.wb.first;
+        const uint64_t first = fg < G ? (uint64_t)gpos[fg] : in_list;  // past the list every term is below min_p
+        if (first < keep) keep = first > 1 ? first : 1;
+    }
+    if (keep > in_list) keep = in_list;  // more only with NaN logits, outside the reference's contract
+    // :236-242 temperature weights and their total over keep, then the draw (:270-275)
+    int gk;
+    uint32_t ck;
+    cut(keep, gk, ck);
+    const float inv_t = 1.0f / P.temp;
+    auto wterm = [&](float x) { return zexpf_nb((x - mx) * inv_t); };
+    float total = 0.0f;
+    walk_block(gval, gcnt, gpos, gk, ck, wterm, kWalkSum, 0.0f, total, &sg, &sc, L.wb);
+    const float u0 = P.uniforms[2 * row];
+    float r = u0 * total;
+    if (walk_block(gval, gcnt, gpos, gk, ck, wterm, kWalkDrop, 0.0f, r, &sg, &sc, L.wb) < 0) {
+        sg = gk;  // none reaches r <= 0: the last kept entry
+        sc = (int64_t)ck - 1;
+    }
+    // the entry's index among all entries of its value (equal groups are adjacent)
+    const float vt = gval[sg];
+    int64_t idx = sc;
+    for (int g = sg - 1; g >= 0 && gval[g] == vt; --g) idx += gcnt[g];
+    __syncthreads();  // every thread is done with gpos (its space becomes vbits)
 
     // 7. the drawn entry's id: the (idx+1)-th entry of value vt in id order.
     //    One read of the row counts each 4096-id tile's entries of value vt
     //    (kWholeBatch vectors in flight per thread); the tile that holds the
     //    entry is read again and ranked.
-    const float vt = L.f[0];
-    const int64_t idx = L.i64[0];
-    const int64_t keep = L.i64[1];
     const int ntile = (nvec + kThreads - 1) / kThreads;
     auto vhit = [&](const uint4 &raw, uint32_t mword, int q) -> uint32_t {  // entries of value vt in vector q
         float v[VEC];
