@@ -54,7 +54,7 @@ struct WholeLds {
     union {
         struct {                         // steps 2-5
             uint32_t kbits[65536 / 32];  // present keys
-            uint32_t wsuf[65536 / 32];   // present keys (at or above the floor) in words above each word
+            uint2 kw[65536 / 32];        // per word: its present keys at or above the floor, and how many are in words above
             uint32_t bcnt[kWholeKeys];   // entries per key rank
             uint16_t bkey[kWholeKeys];   // key of each rank
         } k;
@@ -466,7 +466,7 @@ __global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
                 top2_merge(t1, t2, x);
                 const uint32_t k = key16(x);
                 const uint32_t bit = 1u << (k & 31);
-                if (!(L.w.k.kbits[k >> 5] & bit)) atomicOr(&L.w.k.kbits[k >> 5], bit);
+                atomicOr(&L.w.k.kbits[k >> 5], bit);  // no return: nothing waits on it
             }
         }
     }
@@ -549,8 +549,8 @@ __global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
 #pragma unroll
     for (int j = 3; j >= 0; --j) {  // words in descending order within this thread
         const uint32_t w = (uint32_t)(4 * tid + j);
-        L.w.k.wsuf[w] = above;
         uint32_t bits = L.w.k.kbits[w];
+        L.w.k.kw[w] = make_uint2(bits, above);
         uint32_t r = above;
         while (bits) {  // highest key first
             const int b = 31 - __clz(bits);
@@ -594,8 +594,8 @@ __global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
                 if (x != x) continue;
                 const uint32_t k = key16(x);
                 if (k < kmin) continue;
-                const uint32_t w = k >> 5, above_in = L.w.k.kbits[w] >> (k & 31) >> 1;
-                atomicAdd(&L.w.k.bcnt[L.w.k.wsuf[w] + (uint32_t)__popc(above_in)], 1u);
+                const uint2 kw = L.w.k.kw[k >> 5];  // one read: the word's keys and the count above it
+                atomicAdd(&L.w.k.bcnt[kw.y + (uint32_t)__popc(kw.x >> (k & 31) >> 1)], 1u);
             }
         }
     }
