@@ -43,6 +43,7 @@ def parse():
                     help="final-logit softcap fused into the read (sample path; 0 = off, the config's default)")
     ap.add_argument("--min-p", type=float, default=None,
                     help="override the config's min_p (config 5 with 0 is the whole-order nucleus case)")
+    ap.add_argument("--top-k", type=int, default=None, help="override the config's top_k")
     ap.add_argument("--pruned", type=int, default=0,
                     help="pruned rows (sample path): 64 fixed + this many random groups of 8 ids per row are the "
                          "only logits (zi_sample_rows_pruned; the reference keeps 512); 0 = dense rows")
@@ -603,6 +604,9 @@ def main():
     if args.min_p is not None:
         w.params = dict(w.params, min_p=args.min_p)
         w.name += f"_minp{args.min_p:g}"
+    if args.top_k is not None:
+        w.params = dict(w.params, top_k=args.top_k)
+        w.name += f"_k{args.top_k}"
     if args.config == 4:
         bench_entropy(args, w)
         return
@@ -665,6 +669,11 @@ def main():
         kernel = "pruned_kernel"
     elif rows >= 256:
         kernel = "prefix_kernel" if (k_eff > 256 and w.params.get("min_p", 0.05) > 0) else "row_kernel"
+        if (k_eff > 256 and w.params.get("min_p", 0.05) == 0 and w.bf16 and args.softcap <= 0
+                and not w.params.get("xtc_probability", 0)):
+            # no prefix settles these rows: row_kernel's top-256 pass, then the sort-free whole-order
+            # pass, which takes most of the call (achieved is over the whole call)
+            kernel = "whole_kernel"
     else:
         kernel = "nucleus_kernel" if k_eff > 256 else "sample_kernel"
     traffic = read_traffic(args.traffic, kernel, w.name)
