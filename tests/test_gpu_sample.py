@@ -182,20 +182,28 @@ def test_large_batch_rows(ctx, oracle, rows, V, k, kind, pen, mask):
 LATE_SCENES = ["leaders", "all_leaders", "neg_edit", "nan_free_mix", "rp_below_one"]
 
 
+# config 2's k; the largest k with the per-wave candidate threshold (kTauWaveMaxK
+# = 58, zi_rowpass.hpp) and the first with the bisection; the largest k with the
+# late select (kLatePenMaxK = 64, zi_sample_kernels.hpp) and the first without
+LATE_KS = [50, 58, 59, 64, 65]
+
+
+@pytest.mark.parametrize("top_k", LATE_KS)
 @pytest.mark.parametrize("scene", LATE_SCENES)
-def test_late_penalty_select(ctx, oracle, scene):
+def test_late_penalty_select(ctx, oracle, scene, top_k):
     """Penalties that never raise a logit are applied to the chunk's raw
     candidates only; when penalized leaders drop below the candidate
     threshold (or an edit delta is negative) the kernel penalizes its
-    registers and selects again.  Both branches must match the oracle."""
-    rng = np.random.Generator(np.random.PCG64(4200 + LATE_SCENES.index(scene)))
+    registers and selects again.  Both branches must match the oracle, on
+    both sides of the threshold and late-select cutoffs."""
+    rng = np.random.Generator(np.random.PCG64(4200 + LATE_SCENES.index(scene) + 10 * LATE_KS.index(top_k)))
     rows, V = 16, 128256  # 64 workgroups: the late-penalty select is taken from that grid size
     x = (rng.standard_t(3, (rows, V)) * 2).astype(np.float32)
     u = rng.random((rows, 2), dtype=np.float32)
     order = np.argsort(-x, axis=1, kind="stable")
     H = 256
     hist = rng.integers(0, V, (rows, H), dtype=np.uint32)
-    pk = dict(temp=0.7, top_k=50, top_p=0.9, min_p=0.05, repeat_penalty=1.15, freq_penalty=0.3,
+    pk = dict(temp=0.7, top_k=top_k, top_p=0.9, min_p=0.05, repeat_penalty=1.15, freq_penalty=0.3,
               presence_penalty=0.5, penalty_last_n=256)
     ei = ed = ec = None
     if scene == "leaders":  # a few leaders penalized: candidates stay >= k

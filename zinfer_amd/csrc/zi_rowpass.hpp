@@ -451,21 +451,28 @@ __device__ __forceinline__ float owned_value(const RowSource &a, const PenTable 
 
 // --------------------------------------------------------- stage A select
 // Candidate threshold tau <= the chunk's k-th largest value, from the lane
-// maxima (distinct elements of the chunk).  k <= 64: each wave sorts its 64
-// lane maxima and contributes its r largest, r = max(ceil(k/W), 64/W); the
-// union holds W*r >= k elements, so its k-th largest is a lower bound of the
-// chunk's k-th largest.  k > 64: every lane maximum enters the union (a
-// tighter bound than per-wave top-r lists), and wave 0 bisects the top 20
-// key bits for the largest T with at least k union keys >= T.  Lanes without
-// a value contribute okey(-inf) (a bound at -inf admits everything).
-// Penalized elements diverted from the stream are not in the union, which
-// only lowers the bound.  Contains two barriers.
+// maxima (distinct elements of the chunk).  k <= kTauWaveMaxK: each wave
+// sorts its 64 lane maxima and contributes its r largest, r = max(ceil(k/W),
+// 64/W); the union holds W*r >= k elements, so its k-th largest is a lower
+// bound of the chunk's k-th largest.  Larger k: every lane maximum enters the
+// union, and wave 0 bisects the top 20 key bits for the largest T with at
+// least k union keys >= T (valid for any k).  Lanes without a value
+// contribute okey(-inf) (a bound at -inf admits everything).  Penalized
+// elements diverted from the stream are not in the union, which only lowers
+// the bound.  Contains two barriers.
+//
+// The per-wave union has 64 entries, so as k nears 64 its k-th largest falls
+// to about the smallest of 8 per-wave 8th maxima and admits many candidates.
+// Config-2 rows (64 x 128256 f32, penalties), us per call, per-wave against
+// bisection: k = 40 16.4 / 17.5, k = 56 17.1 / 18.3, k = 58 17.4 / ~18.3,
+// k = 60 19.0 / 18.3, k = 64 48.4 / 18.4.
+constexpr int kTauWaveMaxK = 58;
 constexpr int kMaxR = 64;  // union entries per wave
 
 __device__ __forceinline__ float chunk_tau(float m1, int k, uint32_t *uni, uint32_t *s_tau) {
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const uint32_t mkey = (m1 == m1) ? okey(m1) : 0u;
-    if (k <= 64) {
+    if (k <= kTauWaveMaxK) {
         const int r = max((k + kWaves - 1) / kWaves, 64 / kWaves);
         const uint32_t key = wave_sort_desc_u32(mkey);
         if (lane < r) uni[wid * r + lane] = key;
@@ -475,7 +482,7 @@ __device__ __forceinline__ float chunk_tau(float m1, int k, uint32_t *uni, uint3
     __syncthreads();
     if (wid == 0) {
         uint32_t t;
-        if (k <= 64) {
+        if (k <= kTauWaveMaxK) {
             const int U = kWaves * max((k + kWaves - 1) / kWaves, 64 / kWaves);
             const uint32_t u = wave_sort_desc_u32(lane < U ? uni[lane] : 0u);
             t = (uint32_t)__builtin_amdgcn_readlane((int)u, k - 1);
@@ -629,7 +636,7 @@ constexpr int kWaveCand = 64;  // candidates per wave region
 template <typename T, int NV>
 struct SelectLds {
     static constexpr int VEC = VecTraits<T>::VEC;
-    uint32_t uni[kWaves * kMaxR];  // threshold union (all lane maxima for k > 64)
+    uint32_t uni[kWaves * kMaxR];  // threshold union (all lane maxima for k > kTauWaveMaxK)
     float sx[kWaves][kStageCap * 2 * VEC];  // staged vector pairs
     uint32_t sid[kWaves][kStageCap * 2];
     uint64_t wkey[kWaves][kWaveCand];  // candidates, one region per wave

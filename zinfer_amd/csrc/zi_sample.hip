@@ -32,13 +32,12 @@ static hipError_t launch_sample_t(const SampleParams &P, int rows, hipStream_t s
         // (config 1, 4 workgroups, measured 0.13 us faster with the
         // in-stream penalties; config 2, 256 workgroups, 0.72 us slower).
         const RowSource &a = P.src;
-        // The late select relies on few raw candidates.  Its threshold is the
-        // k-th of 64 per-wave lane maxima (k <= 64) or of all of them, so it
-        // loosens as k grows, and once the candidates overflow the per-wave
-        // staging the late select selects again.  Measured on config-2 rows:
-        // k = 50 16.6 us late against 17.5 in-stream; k = 51 16.7 late
-        // against 17.2; k = 64 51.5 late against 32.5 in-stream; k = 100
-        // 37.1 late against 24.0.  The crossover lies between 51 and 64.
+        // The late select relies on few raw candidates: once they overflow
+        // the per-wave staging it selects again.  Measured on config-2 rows
+        // (64 x 128256 f32, penalties), us per call, late against in-stream:
+        // k = 32 15.9 / 16.6, k = 48 16.8 / 17.6, k = 58 17.4 / 18.1,
+        // k = 60 18.3 / 18.8, k = 64 18.4 / 18.8 (k = 60 and 64 with the
+        // bisection threshold), k = 100 37.1 / 24.0.
         const bool late = rows * a.G >= kLatePenMinGroups && P.k <= kLatePenMaxK && (!a.do_rep || a.rp >= 1.0f) &&
                           (!a.do_fp || (a.freq >= 0.0f && a.pres >= 0.0f));
         if (late) hipLaunchKernelGGL((sample_kernel<T, NV, M, PN, CAP, true>), grid, block, 0, st, P);

@@ -22,7 +22,7 @@ namespace zi {
 
 constexpr int kRowLoopRows = kRowLoopRowsHost;  // batches this large run one workgroup per row
 constexpr int kLatePenMinGroups = 64;  // grids from a quarter of the CUs take the late-penalty select
-constexpr int kLatePenMaxK = 50;  // largest top_k measured faster with the late select
+constexpr int kLatePenMaxK = 64;  // largest top_k measured faster with the late select (k = 100 is slower)
 
 template <bool P>
 struct PenLds {
