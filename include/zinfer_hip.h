@@ -376,6 +376,14 @@ void     zi_adaptive_draft_record_margin(zi_adaptive_draft *a, float margin);   
 uint64_t zi_adaptive_draft_next(zi_adaptive_draft *a);                           /* :388 */
 void     zi_adaptive_draft_update(zi_adaptive_draft *a, uint64_t accepted, uint64_t drafted,
                                   int32_t has_margin, float margin);             /* :408 */
+/* The entropy signal for the same controller (no counterpart in the reference,
+ * whose controller reads the logit margin only; the entropy comes from
+ * zi_entropy_topk_rows).  zi_entropy_margin(H) is the margin m >= 0 at which
+ * the two-token softmax [m, 0] has entropy H nats: 0 for H >= ln 2 or NaN,
+ * capped at 100 for H near 0.  record_entropy records that margin, so
+ * nextDraft's thresholds (3.0, 1.8, 0.9) act at H = 0.191, 0.408, 0.601. */
+float    zi_entropy_margin(float entropy);
+void     zi_adaptive_draft_record_entropy(zi_adaptive_draft *a, float entropy);
 
 #ifdef __cplusplus
 }

@@ -115,6 +115,44 @@ def test_adaptive_draft_kat():
     assert L.zi_adaptive_draft_next(C.byref(a)) == 1
 
 
+def test_entropy_margin_inverts_two_token_entropy():
+    """zi_entropy_margin(H) is the m at which softmax([m, 0]) has entropy H:
+    checked against scipy's entropy of that distribution (a round trip), its
+    boundaries and its monotonicity."""
+    from scipy.stats import entropy
+
+    from zinfer_amd._lib import lib
+
+    L = lib()
+    for m in [0.0, 0.05, 0.5, 0.9, 1.8, 3.0, 7.5, 20.0, 30.0]:  # in f64, p[0] rounds to 1 beyond ~35
+        p = np.exp(np.array([m, 0.0]) - m)
+        H = float(entropy(p / p.sum()))
+        got = L.zi_entropy_margin(H)
+        assert abs(got - m) <= 1e-4 * max(1.0, m), (m, H, got)
+    assert L.zi_entropy_margin(float(np.log(2.0))) == 0.0
+    assert L.zi_entropy_margin(5.0) == 0.0  # a flatter row than any two-token one
+    assert L.zi_entropy_margin(float("nan")) == 0.0
+    assert L.zi_entropy_margin(0.0) == 100.0
+    hs = np.linspace(1e-6, 0.69, 200).astype(np.float32)
+    ms = np.array([L.zi_entropy_margin(float(h)) for h in hs])
+    assert np.all(np.diff(ms) < 0)
+
+
+def test_adaptive_draft_entropy_input():
+    """record_entropy drives nextDraft exactly as the equivalent margin does."""
+    from zinfer_amd._lib import ZiAdaptiveDraft, lib
+
+    L = lib()
+    for H, want in [(0.05, 4), (0.3, 3), (0.5, 3), (0.65, 1), (2.0, 1)]:  # cur_k = 3 after init
+        a = ZiAdaptiveDraft()
+        L.zi_adaptive_draft_init(C.byref(a), 8)
+        L.zi_adaptive_draft_record_entropy(C.byref(a), H)
+        b = ZiAdaptiveDraft()
+        L.zi_adaptive_draft_init(C.byref(b), 8)
+        L.zi_adaptive_draft_record_margin(C.byref(b), L.zi_entropy_margin(H))
+        assert L.zi_adaptive_draft_next(C.byref(a)) == L.zi_adaptive_draft_next(C.byref(b)) == want, H
+
+
 def test_invalid_arguments_fail_loudly():
     """Entry points reject bad arguments with a status and a message, never
     silently; without a GPU, zi_create reports the missing device."""

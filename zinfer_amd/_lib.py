@@ -169,6 +169,8 @@ SIGNATURES = {
     "zi_adaptive_draft_init": (None, [C.POINTER(ZiAdaptiveDraft), C.c_uint64]),
     "zi_adaptive_draft_record_margin": (None, [C.POINTER(ZiAdaptiveDraft), C.c_float]),
     "zi_adaptive_draft_next": (C.c_uint64, [C.POINTER(ZiAdaptiveDraft)]),
+    "zi_entropy_margin": (C.c_float, [C.c_float]),
+    "zi_adaptive_draft_record_entropy": (None, [C.POINTER(ZiAdaptiveDraft), C.c_float]),
     "zi_adaptive_draft_update": (None, [C.POINTER(ZiAdaptiveDraft), C.c_uint64, C.c_uint64, C.c_int32,
                                         C.c_float]),
 }

@@ -662,6 +662,31 @@ extern "C" void zi_adaptive_draft_init(zi_adaptive_draft *a, uint64_t max_k) {
 extern "C" void zi_adaptive_draft_record_margin(zi_adaptive_draft *a, float m) {
     if (a) a->last_margin = m;
 }
+// The controller's entropy input (the reference reads the margin only): the
+// margin m >= 0 at which the two-token softmax [m, 0] has entropy H (nats),
+//   H2(m) = ln(1 + e^-m) + m e^-m / (1 + e^-m),
+// strictly decreasing from ln 2 at m = 0 towards 0.  Inverted by bisection
+// in f64; H >= ln 2 (or NaN) gives 0, H <= H2(kMaxEquivMargin) gives that cap.
+static constexpr double kMaxEquivMargin = 100.0;
+static double entropy_two_token(double m) {
+    const double e = std::exp(-m);
+    return std::log1p(e) + m * e / (1.0 + e);
+}
+extern "C" float zi_entropy_margin(float entropy) {
+    const double H = (double)entropy;
+    if (!(H < std::log(2.0))) return 0.0f;  // also NaN
+    if (H <= entropy_two_token(kMaxEquivMargin)) return (float)kMaxEquivMargin;
+    double lo = 0.0, hi = kMaxEquivMargin;  // H2(lo) > H >= H2(hi)
+    for (int i = 0; i < 80; ++i) {
+        const double mid = 0.5 * (lo + hi);
+        if (entropy_two_token(mid) > H) lo = mid;
+        else hi = mid;
+    }
+    return (float)(0.5 * (lo + hi));
+}
+extern "C" void zi_adaptive_draft_record_entropy(zi_adaptive_draft *a, float entropy) {
+    if (a) a->last_margin = zi_entropy_margin(entropy);
+}
 extern "C" uint64_t zi_adaptive_draft_next(zi_adaptive_draft *a) {
     if (!a) return 0;
     if (a->cooldown_steps > 0) {  // gen.zig:388-405
