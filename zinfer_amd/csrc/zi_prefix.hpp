@@ -159,7 +159,8 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 // (no maximum, no candidate, no weight).
 template <typename T, bool HAS_MASK, bool HAS_PEN, bool CAP>
 __device__ __forceinline__ void prefix_prep(const RowSource &a, const PrefixLds &L, uint4 raw, uint32_t mword,
-                                            int id0, int lim_id, float (&v)[VecTraits<T>::VEC]) {
+                                            int id0, int lim_id, float (&v)[VecTraits<T>::VEC],
+                                            const uint32_t *pword = nullptr) {
     constexpr int VEC = VecTraits<T>::VEC;
     unpack<T>(raw, v);
     if constexpr (CAP) {
@@ -173,7 +174,7 @@ __device__ __forceinline__ void prefix_prep(const RowSource &a, const PrefixLds 
     }
     const int lim = lim_id - id0;
     if (HAS_PEN && lim > 0) {
-        const uint32_t pb = (L.bits[id0 >> 5] >> (id0 & 31)) & ((1u << VEC) - 1u);
+        const uint32_t pb = ((pword ? *pword : L.bits[id0 >> 5]) >> (id0 & 31)) & ((1u << VEC) - 1u);
         if (pb) {
 #pragma unroll
             for (int e = 0; e < VEC; ++e) v[e] = ((pb >> e) & 1u) ? -INFINITY : v[e];
@@ -351,11 +352,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         const int n0 = c1, n1 = min(V, c1 + SUB);  // the next step
         const int nvec_next = (n1 - n0 + VEC - 1) / VEC;
         float lmax = -INFINITY;
+        uint32_t pwv[NV];  // the step's penalty-bit words, read together
+#pragma unroll
+        for (int j = 0; j < NV; ++j)
+            pwv[j] = HAS_PEN ? L.bits[min(c0 + (j * kThreads + tid) * VEC, V - 1) >> 5] : 0u;
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
             const int id0 = c0 + (j * kThreads + tid) * VEC;
             float v[VEC];
-            prefix_prep<T, HAS_MASK, HAS_PEN, CAP>(a, L, raw[j], HAS_MASK ? mw[j] : 0u, id0, c1, v);
+            prefix_prep<T, HAS_MASK, HAS_PEN, CAP>(a, L, raw[j], HAS_MASK ? mw[j] : 0u, id0, c1, v, &pwv[j]);
             if (n0 < n1) {  // uniform: the same vector of the next step
                 const int nq = min(j * kThreads + tid, nvec_next - 1);
                 raw[j] = ld_stream(reinterpret_cast<const uint4 *>(lrow + n0 + nq * VEC));
