@@ -89,10 +89,7 @@ __device__ __forceinline__ void exact_vector(const RowSource &a, int row, const 
     const T *base = reinterpret_cast<const T *>(a.logits) + (int64_t)row * a.ld;
     const int id0 = q * VEC;
     unpack<T>(*reinterpret_cast<const uint4 *>(base + id0), v);
-    if constexpr (CAP) {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) v[e] = softcap_at(a, id0 + e, v[e]);
-    }
+    if constexpr (CAP) softcap_vec<VEC>(a, id0, v);
     if (HAS_MASK) {
         const uint32_t mb = a.mask[(int64_t)row * a.mask_ld + (id0 >> 5)] >> (id0 & 31);
 #pragma unroll

@@ -163,10 +163,7 @@ __device__ __forceinline__ void prefix_prep(const RowSource &a, const PrefixLds 
                                             const uint32_t *pword = nullptr) {
     constexpr int VEC = VecTraits<T>::VEC;
     unpack<T>(raw, v);
-    if constexpr (CAP) {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) v[e] = softcap_at(a, id0 + e, v[e]);
-    }
+    if constexpr (CAP) softcap_vec<VEC>(a, id0, v);
     if (HAS_MASK) {
         const uint32_t mb = mword >> (id0 & 31);
 #pragma unroll

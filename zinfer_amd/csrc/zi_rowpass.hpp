@@ -89,6 +89,37 @@ __device__ __forceinline__ bool row_ticket(int32_t *tickets, int row, int G, int
 __device__ __forceinline__ float softcap_at(const RowSource &a, int id, float v) {
     return id < a.cap_body ? softcap_f(v, a.cap, a.inv_cap) : softcap_tail_f(v, a.cap);
 }
+// The softcap of the vector [id0, id0 + VEC): the scalar tail (and its f64
+// tanh) only in the one vector that reaches the row's last ids, behind a
+// branch, so that the per-element code stays small enough to unroll (and the
+// chunk's registers stay registers).
+template <int VEC>
+struct FVec {
+    float x[VEC];
+};
+// Out of line (by value, so no array's address escapes the caller).
+template <int VEC>
+__device__ __attribute__((noinline)) FVec<VEC> softcap_vec_tail(FVec<VEC> v, int id0, int cap_body, float cap,
+                                                                 float inv_cap) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e)
+        v.x[e] = id0 + e < cap_body ? softcap_f(v.x[e], cap, inv_cap) : softcap_tail_f(v.x[e], cap);
+    return v;
+}
+template <int VEC>
+__device__ __forceinline__ void softcap_vec(const RowSource &a, int id0, float (&v)[VEC]) {
+    if (id0 + VEC <= a.cap_body) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) v[e] = softcap_f(v[e], a.cap, a.inv_cap);
+    } else {
+        FVec<VEC> t;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) t.x[e] = v[e];
+        t = softcap_vec_tail<VEC>(t, id0, a.cap_body, a.cap, a.inv_cap);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) v[e] = t.x[e];
+    }
+}
 
 // --------------------------------------------------------- penalty table
 struct PenTable {
@@ -402,10 +433,7 @@ __device__ __forceinline__ float chunk_stream(const RowSource &a, int row, int c
                 raw[j] = ld_stream(reinterpret_cast<const uint4 *>(base_next + nq * VEC));
             }
         }
-        if constexpr (CAP) {
-#pragma unroll
-            for (int e = 0; e < VEC; ++e) v[e] = softcap_at(a, id0 + e, v[e]);
-        }
+        if constexpr (CAP) softcap_vec<VEC>(a, id0, v);
         if (HAS_MASK) {
             uint32_t mb = mw[j] >> (id0 & 31);
 #pragma unroll
@@ -987,12 +1015,33 @@ __device__ __forceinline__ int pen_find(const PenTable &t, uint32_t id, int hs_l
     }
 }
 
+// Upper bound of the final-logit softcap of every value below tau (f32 body
+// or scalar tail, src/model.zig:2492-2513): cap tanh(tau / cap) in f64 plus
+// cap 2^-17, rounded up.  The exact function is monotone; the f32 forms stay
+// within cap 2^-22 of it (the body) and a few ulps (the tail), and the body's
+// argument rounding moves tanh by at most cap 9 2^-23 inside its +-9 clamp.
+// Below tau = -9 cap (and for tau = -inf or NaN) the body's clamp maps -inf
+// to -cap tanh(9), above cap tanh(tau / cap): no bound, *ok = false.
+__device__ __forceinline__ float softcap_upper(const RowSource &a, float tau, bool *ok) {
+    *ok = tau > -9.0f * a.cap;
+    const double cp = (double)a.cap;
+    const double e = cp * tanh((double)tau / cp) + cp * 0x1p-17;
+    float u = (float)e;
+    if ((double)u < e) u = nextafterf(u, INFINITY);
+    return u;
+}
+
 // The chunk's selection after chunk_stream without penalties: `tau` from
 // select_prepare (raw lane maxima), `pr` from pen_prefetch, hl_raw / ne_raw
 // the row's hist_len / edit_count as loaded, `t` cleared by pen_clear_hash
 // before a barrier that precedes this call, *s_bad zero.  Publishes the
 // chunk's exact penalized top-k like chunk_select_publish.
-template <typename T, int NV>
+// CAPC (a final-logit softcap): the stream ran without it, and only the
+// candidates are capped (then penalized).  A value outside C is below tau,
+// so its capped value is below tc = softcap_upper(tau) and its penalized one
+// too; with at least k candidates >= tc the top-k lie in C.  Otherwise the
+// chunk is streamed again with the softcap and selected as before.
+template <typename T, int NV, bool CAPC = false, bool HAS_MASK = false>
 __device__ __forceinline__ void chunk_select_late(const RowSource &a, int row, ChunkRegs<T, NV> &cr, int c0, int c1,
                                                   int k, SelectLds<T, NV> &sl, PenTable &t, PenRegs &pr, int hl_raw,
                                                   int ne_raw, uint32_t *s_tau, int *s_n, int *s_bad, uint32_t *bins,
@@ -1004,10 +1053,12 @@ __device__ __forceinline__ void chunk_select_late(const RowSource &a, int row, C
     pen_window(rp, pr);
     if (pen_count_late(t, rp, pr, c0, c1)) *s_bad = 1;
     if (lane == 0) sl.wcnt[wid] = wc;
+    bool cap_ok = true;
+    const float tc = CAPC ? softcap_upper(a, tau, &cap_ok) : tau;  // uniform
     __syncthreads();  // hash, wave counts and the bad-edit flag complete
     int off[kWaves + 1];
     off[0] = 0;
-    bool overflow = *s_bad != 0;
+    bool overflow = *s_bad != 0 || !cap_ok;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
         overflow |= sl.wcnt[w] > kWaveCand;
@@ -1018,16 +1069,21 @@ __device__ __forceinline__ void chunk_select_late(const RowSource &a, int row, C
         bool ge = false;
         if (lane < nw) {
             float x = sl.wval[wid][lane];
+            const uint32_t id = ckey_id(sl.wkey[wid][lane]);
+            bool upd = CAPC;
+            if constexpr (CAPC) x = softcap_at(a, (int)id, x);
             if (rp.any) {
-                const uint32_t id = ckey_id(sl.wkey[wid][lane]);
                 const int h = pen_find(t, id, rp.hs_log2);
                 if (h >= 0) {
                     x = pen_apply(x, t.cnt[h], t.delta[h], a);
-                    sl.wkey[wid][lane] = ckey(x, id);
-                    sl.wval[wid][lane] = x;
+                    upd = true;
                 }
             }
-            ge = x >= tau;
+            if (upd) {
+                sl.wkey[wid][lane] = ckey(x, id);
+                sl.wval[wid][lane] = x;
+            }
+            ge = x >= tc;
         }
         const uint64_t b = ballot(ge);
         if (lane == 0) sl.wge[wid] = __popcll(b);
@@ -1043,6 +1099,7 @@ __device__ __forceinline__ void chunk_select_late(const RowSource &a, int row, C
     // Fallback: penalize the registers (every element probes the hash) and
     // select from scratch.  select_prepare's barriers order its LDS writes
     // after every read above.
+    if constexpr (CAPC) chunk_stream<T, NV, HAS_MASK, false, true>(a, row, c0, c1, cr, nullptr, nullptr);
     if (rp.any) {
         float tmax = -INFINITY;
 #pragma unroll

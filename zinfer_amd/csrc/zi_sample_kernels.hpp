@@ -63,7 +63,7 @@ __device__ __forceinline__ void sample_stage_b(const SampleParams &P, int row, i
 
 // LATE (with HAS_PEN, for penalties that never raise a logit): the stream
 // runs without the penalty inputs and only the chunk's candidates are
-// penalized (chunk_select_late).
+// penalized (chunk_select_late); with CAP, only they are softcapped as well.
 template <typename T, int NV, bool HAS_MASK, bool HAS_PEN, bool CAP, bool LATE>
 __global__ __launch_bounds__(kThreads) void sample_kernel(SampleParams P) {
     __shared__ union {
@@ -108,13 +108,14 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleParams P) {
             pen_clear_hash(*pen);  // ordered before the inserts by the barriers below
             tau = select_prepare<T, NV>(lmax, k, sm.a.sel, s_tau, &s_n);
         };
-        chunk_stream<T, NV, HAS_MASK, false, CAP, NoHook, kSplit>(a, row, c0, c1, cr, nullptr, nullptr, NoHook(),
-                                                                   mid);
+        // with a softcap, the stream stays raw and only the candidates are capped
+        chunk_stream<T, NV, HAS_MASK, false, false, NoHook, kSplit>(a, row, c0, c1, cr, nullptr, nullptr, NoHook(),
+                                                                     mid);
         int ur = 2 * row;
         asm volatile("" : "+v"(ur));
         const float u0 = P.uniforms[ur], u1 = P.uniforms[ur + 1];
-        chunk_select_late<T, NV>(a, row, cr, c0, c1, k, sm.a.sel, *pen, pr, hl_raw, ne_raw, s_tau, &s_n, &s_bad,
-                                 s_bins, s_dig, out, tau);
+        chunk_select_late<T, NV, CAP, HAS_MASK>(a, row, cr, c0, c1, k, sm.a.sel, *pen, pr, hl_raw, ne_raw, s_tau,
+                                                &s_n, &s_bad, s_bins, s_dig, out, tau);
         if (!row_ticket(P.tickets, row, G, &s_flag)) return;
         sample_stage_b(P, row, G, k, sm.b, u0, u1);
         return;
