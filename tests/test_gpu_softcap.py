@@ -85,24 +85,27 @@ LATE_KINDS = ["normal", "t3", "wide", "neginf", "flat_top", "huge"]
 @pytest.mark.parametrize("cap", [30.0, 4.0])
 @pytest.mark.parametrize("kind", LATE_KINDS)
 @pytest.mark.parametrize("mask", [False, True])
-def test_softcap_late_select(ctx, oracle, kind, mask, cap):
-    """Grids of >= 64 workgroups with penalties that never raise a logit cap
-    only the chunk's raw candidates (chunk_select_late with CAPC): exact when
+@pytest.mark.parametrize("pen", [True, False])
+def test_softcap_late_select(ctx, oracle, kind, mask, cap, pen):
+    """Chunked top-k rows cap only the chunk's raw candidates
+    (chunk_select_late with CAPC): with penalties that never raise a logit on
+    grids of >= 64 workgroups, and without penalties on any grid.  Exact when
     at least k capped candidates reach the bound on every other capped value,
     else the chunk is streamed again with the softcap.  Saturated rows
     ("wide", "huge": many values far beyond the cap tie after capping),
     -inf-heavy rows and a negative edit force that fallback."""
     rows, V = 16, 128256  # 4 chunks per row: 64 workgroups
-    rng = np.random.Generator(np.random.PCG64(3300 + LATE_KINDS.index(kind) + (20 if mask else 0)))
+    rng = np.random.Generator(np.random.PCG64(3300 + LATE_KINDS.index(kind) + (20 if mask else 0) + (40 if pen else 0)))
     kx = "normal" if kind in ("flat_top", "huge") else kind
-    x, hist, hl, m, ei, ed, ec = _inputs(rng, rows, V, kx, True, mask, True)
+    x, hist, hl, m, ei, ed, ec = _inputs(rng, rows, V, kx, pen, mask, pen)
     if kind == "flat_top":  # integer logits: raw ties, and capped ties among them
         x = np.round(x).astype(np.float32)
     elif kind == "huge":  # far beyond 9 caps: the body's clamp makes every capped value equal
         x = (x * 100 + 500).astype(np.float32)
-    ed[::3, 0] = -5.0  # an edit that raises a logit: that chunk's fallback
-    pk = dict(temp=0.7, top_k=50, top_p=0.9, min_p=0.05, repeat_penalty=1.15, freq_penalty=0.3,
-              presence_penalty=0.5, penalty_last_n=256, final_logit_softcap=cap)
+    pk = dict(temp=0.7, top_k=50, top_p=0.9, min_p=0.05, final_logit_softcap=cap)
+    if pen:
+        ed[::3, 0] = -5.0  # an edit that raises a logit: that chunk's fallback
+        pk.update(repeat_penalty=1.15, freq_penalty=0.3, presence_penalty=0.5, penalty_last_n=256)
     u = rng.random((rows, 2), dtype=np.float32)
     g = gpu_sample(ctx, pk, x, u, hist, hl, m, ei, ed, ec)
     o = oracle_sample(oracle, pk, x, u, hist, hl, m, ei, ed, ec)

@@ -1041,24 +1041,32 @@ __device__ __forceinline__ float softcap_upper(const RowSource &a, float tau, bo
 // so its capped value is below tc = softcap_upper(tau) and its penalized one
 // too; with at least k candidates >= tc the top-k lie in C.  Otherwise the
 // chunk is streamed again with the softcap and selected as before.
-template <typename T, int NV, bool CAPC = false, bool HAS_MASK = false>
+// PENL = false (a softcap without penalties or edits): no hash; t, pr and
+// s_bad are not used.
+template <typename T, int NV, bool CAPC = false, bool HAS_MASK = false, bool PENL = true>
 __device__ __forceinline__ void chunk_select_late(const RowSource &a, int row, ChunkRegs<T, NV> &cr, int c0, int c1,
-                                                  int k, SelectLds<T, NV> &sl, PenTable &t, PenRegs &pr, int hl_raw,
+                                                  int k, SelectLds<T, NV> &sl, PenTable *tp, PenRegs *pr, int hl_raw,
                                                   int ne_raw, uint32_t *s_tau, int *s_n, int *s_bad, uint32_t *bins,
                                                   int *s_dig, ChunkOut out, float tau) {
+    static_assert(PENL || CAPC, "without penalties this select is for capped rows");
     constexpr int VEC = VecTraits<T>::VEC;
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int wc = wave_candidates<T, NV, false>(a, cr, c0, tau, sl, nullptr, nullptr);
-    const RowPen rp = row_pen_from(a, row, row_pen_window_on(a) ? hl_raw : 0, a.edit_ids ? ne_raw : 0);
-    pen_window(rp, pr);
-    if (pen_count_late(t, rp, pr, c0, c1)) *s_bad = 1;
+    RowPen rp;
+    rp.any = false;
+    rp.hs_log2 = 6;
+    if constexpr (PENL) {
+        rp = row_pen_from(a, row, row_pen_window_on(a) ? hl_raw : 0, a.edit_ids ? ne_raw : 0);
+        pen_window(rp, *pr);
+        if (pen_count_late(*tp, rp, *pr, c0, c1)) *s_bad = 1;
+    }
     if (lane == 0) sl.wcnt[wid] = wc;
     bool cap_ok = true;
     const float tc = CAPC ? softcap_upper(a, tau, &cap_ok) : tau;  // uniform
     __syncthreads();  // hash, wave counts and the bad-edit flag complete
     int off[kWaves + 1];
     off[0] = 0;
-    bool overflow = *s_bad != 0 || !cap_ok;
+    bool overflow = (PENL && *s_bad != 0) || !cap_ok;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
         overflow |= sl.wcnt[w] > kWaveCand;
@@ -1072,7 +1080,8 @@ __device__ __forceinline__ void chunk_select_late(const RowSource &a, int row, C
             const uint32_t id = ckey_id(sl.wkey[wid][lane]);
             bool upd = CAPC;
             if constexpr (CAPC) x = softcap_at(a, (int)id, x);
-            if (rp.any) {
+            if (PENL && rp.any) {
+                const PenTable &t = *tp;
                 const int h = pen_find(t, id, rp.hs_log2);
                 if (h >= 0) {
                     x = pen_apply(x, t.cnt[h], t.delta[h], a);
@@ -1100,7 +1109,8 @@ __device__ __forceinline__ void chunk_select_late(const RowSource &a, int row, C
     // select from scratch.  select_prepare's barriers order its LDS writes
     // after every read above.
     if constexpr (CAPC) chunk_stream<T, NV, HAS_MASK, false, true>(a, row, c0, c1, cr, nullptr, nullptr);
-    if (rp.any) {
+    if (PENL && rp.any) {
+        const PenTable &t = *tp;
         float tmax = -INFINITY;
 #pragma unroll
         for (int j = 0; j < NV; ++j) {

@@ -114,8 +114,23 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleParams P) {
         int ur = 2 * row;
         asm volatile("" : "+v"(ur));
         const float u0 = P.uniforms[ur], u1 = P.uniforms[ur + 1];
-        chunk_select_late<T, NV, CAP, HAS_MASK>(a, row, cr, c0, c1, k, sm.a.sel, *pen, pr, hl_raw, ne_raw, s_tau,
+        chunk_select_late<T, NV, CAP, HAS_MASK>(a, row, cr, c0, c1, k, sm.a.sel, pen, &pr, hl_raw, ne_raw, s_tau,
                                                 &s_n, &s_bad, s_bins, s_dig, out, tau);
+        if (!row_ticket(P.tickets, row, G, &s_flag)) return;
+        sample_stage_b(P, row, G, k, sm.b, u0, u1);
+        return;
+    }
+    if constexpr (CAP && !HAS_PEN) {
+        // a softcap without penalties: the stream stays raw and only the
+        // candidates are capped (chunk_select_late without a hash)
+        auto mid = [&](float lmax) { tau = select_prepare<T, NV>(lmax, k, sm.a.sel, s_tau, &s_n); };
+        chunk_stream<T, NV, HAS_MASK, false, false, NoHook, kSplit>(a, row, c0, c1, cr, nullptr, nullptr, NoHook(),
+                                                                     mid);
+        int ur = 2 * row;
+        asm volatile("" : "+v"(ur));
+        const float u0 = P.uniforms[ur], u1 = P.uniforms[ur + 1];
+        chunk_select_late<T, NV, true, HAS_MASK, false>(a, row, cr, c0, c1, k, sm.a.sel, nullptr, nullptr, 0, 0,
+                                                        s_tau, &s_n, nullptr, s_bins, s_dig, out, tau);
         if (!row_ticket(P.tickets, row, G, &s_flag)) return;
         sample_stage_b(P, row, G, k, sm.b, u0, u1);
         return;
