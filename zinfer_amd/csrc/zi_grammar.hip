@@ -42,8 +42,6 @@ struct JsonMaskArgs {
     zi_json_state st[kJsonBatch];
 };
 
-constexpr int kTailRegs = 4;  // tail chunks held in registers (bytes 12-75)
-
 // Walks every lane's piece through step(byte) -> accepted, in lock-step: the
 // chunk and byte counters are wave-uniform (the inline 12 bytes, then tail
 // chunks 1-4 from registers, then chunks loaded as reached), each lane is
@@ -623,8 +621,10 @@ int32_t zi_vocab_create(zi_vocab **out, zi_ctx *ctx, const uint32_t *piece_off, 
 
 void zi_vocab_destroy(zi_vocab *v) {
     if (!v) return;
-    hipSetDevice(v->ctx->device);
-    hipStreamSynchronize(v->ctx->stream);
+    // failures are recorded for zi_last_error; the memory is released anyway
+    hipError_t e = hipSetDevice(v->ctx->device);
+    if (e == hipSuccess) e = hipStreamSynchronize(v->ctx->stream);
+    if (e != hipSuccess) zi_hip_fail(e, "zi_vocab_destroy: device or stream");
     release(v);
 }
 
