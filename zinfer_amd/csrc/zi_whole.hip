@@ -105,148 +105,9 @@ __device__ __forceinline__ void top2_merge(float &t1, float &t2, float x) {
     t1 = fmaxf(t1, x);
 }
 
-__device__ __forceinline__ uint64_t min_u64(uint64_t a, uint64_t b) { return a < b ? a : b; }
-
 __device__ __forceinline__ uint64_t shfl_up_u64(uint64_t v, int o) {
     const uint32_t lo = __shfl_up((uint32_t)v, o), hi = __shfl_up((uint32_t)(v >> 32), o);
     return ((uint64_t)hi << 32) | lo;
-}
-__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l) {
-    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, l), hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), l);
-    return ((uint64_t)hi << 32) | lo;
-}
-
-// One wave walks groups [0, G) over their first `limit` entries (every lane
-// active, uniform result), kWalkPer consecutive groups per lane: each lane
-// composes its groups' maps, the wave scans the lanes' maps, and the lane with
-// the first event walks its own groups to place it.  Returns the entry index
-// at which the walk stops (group *sg, copy *sc), or -1; v is the running value.
-constexpr int kWalkPer = 1;
-
-template <class Term>
-__device__ int64_t walk_groups(const float *gval, const uint32_t *gcnt, int G, uint64_t limit, Term term, int mode,
-                               float thr, float &v, int *sg, int64_t *sc) {
-    const int lane = threadIdx.x & 63;
-    int g = 0;
-    uint64_t cum = 0;
-    while (g < G && cum < limit) {
-        if ((mode != kWalkDrop && v == 0.0f) || (mode == kWalkDrop && !(v > 0.0f))) {  // no grid yet: one group
-            const uint64_t c = min_u64((uint64_t)gcnt[g], limit - cum);
-            const int64_t s = walk_group(v, term(gval[g]), c, mode, thr);
-            if (s >= 0) {
-                *sg = g;
-                *sc = s;
-                return (int64_t)cum + s;
-            }
-            cum += c;
-            ++g;
-            continue;
-        }
-        const WalkGrid gr = walk_grid(v);
-        const uint32_t p0 = gr.m & 1u;
-        const int gb = g + lane * kWalkPer;
-        uint32_t craw[kWalkPer], lraw = 0;
-#pragma unroll
-        for (int k = 0; k < kWalkPer; ++k) {
-            craw[k] = gb + k < G ? gcnt[gb + k] : 0u;
-            lraw += craw[k];
-        }
-        uint32_t rin = lraw;  // inclusive prefix of the lanes' raw counts
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const uint32_t y = __shfl_up(rin, o);
-            if (lane >= o) rin += y;
-        }
-        uint64_t before = cum + (rin - lraw);
-        uint32_t c[kWalkPer], lc = 0;
-        float t[kWalkPer];
-        WalkMap mk[kWalkPer];
-#pragma unroll
-        for (int k = 0; k < kWalkPer; ++k) {  // counts clamped at limit, terms, maps
-            c[k] = before >= limit ? 0u : (uint32_t)min_u64((uint64_t)craw[k], limit - before);
-            before += craw[k];
-            lc += c[k];
-            t[k] = c[k] ? term(gval[gb + k]) : 0.0f;
-            mk[k] = walk_map(walk_term(t[k], gr.qe), c[k]);
-        }
-        WalkMap mp = mk[0];
-#pragma unroll
-        for (int k = 1; k < kWalkPer; ++k) mp = walk_compose(mp, mk[k]);
-        uint32_t par = mp.par0 | (mp.par1 << 1);
-        uint32_t ccl = lc;  // inclusive prefix of the lanes' clamped counts
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {  // inclusive scan: earlier lanes' map, then this lane's
-            WalkMap pm;
-            pm.inc0 = shfl_up_u64(mp.inc0, o);
-            pm.inc1 = shfl_up_u64(mp.inc1, o);
-            const uint32_t pp = __shfl_up(par, o);
-            pm.par0 = pp & 1u;
-            pm.par1 = pp >> 1;
-            const uint32_t yc = __shfl_up(ccl, o);
-            if (lane >= o) {
-                mp = walk_compose(pm, mp);
-                par = mp.par0 | (mp.par1 << 1);
-                ccl += yc;
-            }
-        }
-        // the lanes before this one: their inclusive map and count
-        WalkMap run;
-        run.inc0 = shfl_up_u64(mp.inc0, 1);
-        run.inc1 = shfl_up_u64(mp.inc1, 1);
-        const uint32_t pp = __shfl_up(par, 1);
-        run.par0 = pp & 1u;
-        run.par1 = pp >> 1;
-        uint32_t cex = __shfl_up(ccl, 1);
-        if (lane == 0) {
-            run.inc0 = run.inc1 = 0;
-            run.par0 = 0;
-            run.par1 = 1;
-            cex = 0;
-        }
-        // this lane's first event, if any: its group, the prefix before it
-        int ek = -1;
-        uint64_t pb = 0;
-        uint32_t cb = 0, ce = 0;
-        float te = 0.0f;
-#pragma unroll
-        for (int k = 0; k < kWalkPer; ++k) {
-            const WalkMap nx = walk_compose(run, mk[k]);
-            const uint64_t P = p0 ? nx.inc1 : nx.inc0;
-            if (ek < 0 && c[k] > 0 && walk_event(gr.m, gr.qe, P, mode, thr)) {
-                ek = k;
-                pb = p0 ? run.inc1 : run.inc0;
-                cb = cex;
-                ce = c[k];
-                te = t[k];
-            }
-            cex += c[k];
-            run = nx;
-        }
-        const uint64_t b = ballot(ek >= 0);
-        if (!b) {
-            const uint64_t P63 = readlane_u64(p0 ? mp.inc1 : mp.inc0, 63);
-            v = walk_value(mode == kWalkDrop ? gr.m - P63 : gr.m + P63, gr.qe);
-            cum += (uint32_t)__builtin_amdgcn_readlane(ccl, 63);
-            g += 64 * kWalkPer;
-            continue;
-        }
-        const int L = __ffsll((unsigned long long)b) - 1;
-        const uint64_t Pp = readlane_u64(pb, L);
-        v = walk_value(mode == kWalkDrop ? gr.m - Pp : gr.m + Pp, gr.qe);
-        cum += (uint32_t)__builtin_amdgcn_readlane(cb, L);
-        const int gE = g + L * kWalkPer + __builtin_amdgcn_readlane(ek, L);
-        const float tL = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(te), L));
-        const uint32_t cL = (uint32_t)__builtin_amdgcn_readlane(ce, L);
-        const int64_t s2 = walk_group(v, tL, cL, mode, thr);
-        if (s2 >= 0) {
-            *sg = gE;
-            *sc = s2;
-            return (int64_t)cum + s2;
-        }
-        cum += cL;
-        g = gE + 1;
-    }
-    return -1;
 }
 
 // The whole workgroup walks groups [0, gk], the last of them over its first
