@@ -38,6 +38,14 @@ constexpr int kWholePen = kOwnSlots * kThreads;    // penalized entries (window 
 constexpr int kWholeGroups = kWholeKeys + kWholePen;
 constexpr int kWholeBatch = 16;  // row vectors in flight per thread
 
+// (group, running value) at the start of each step of a block walk
+constexpr int kWalkCp = 64;
+struct WalkCp {
+    int g[kWalkCp];
+    float v[kWalkCp];
+    int n;
+};
+
 struct WholeLds {
     uint32_t pbits[kMaxVocab / 32];  // penalized ids
     union {
@@ -70,6 +78,7 @@ struct WholeLds {
         uint32_t ec;
         int first;
     } wb;
+    WalkCp cp;                   // the top-p total's checkpoints
     float pval[kWholePen];       // penalized entries: value, id (then sorted by value desc, id asc)
     uint32_t pid[kWholePen];
     float sval[kWholePen];
@@ -110,18 +119,29 @@ __device__ __forceinline__ uint64_t shfl_up_u64(uint64_t v, int o) {
     return ((uint64_t)hi << 32) | lo;
 }
 
-// The whole workgroup walks groups [0, gk], the last of them over its first
-// ck entries: a chunk of 512 groups per step, one per thread, the maps scanned
-// over the wave and then across the waves; only the group of the first event
-// is walked on its own (by every thread alike).  Every thread calls it and
-// gets the same result: the entry index at which the walk stops (group *sg,
-// copy *sc), or -1; v is the running value.
+// The whole workgroup walks groups [g, gk] from the running value v, the last
+// group over its first ck entries: a chunk of 512 groups per step, one per
+// thread, the maps scanned over the wave and then across the waves; only the
+// group of the first event is walked on its own (by every thread alike).
+// Every thread calls it and gets the same result: the entry index at which
+// the walk stops (group *sg, copy *sc), or -1; v is the running value.
+// With cp, thread 0 records (group, running value) at the start of every step
+// (up to kWalkCp of them; the count in cp->n after the caller's next barrier).
 template <class Term, class WB>
 __device__ int64_t walk_block(const float *gval, const uint32_t *gcnt, const uint32_t *gpos, int gk, uint32_t ck,
-                              Term term, int mode, float thr, float &v, int *sg, int64_t *sc, WB &W) {
+                              Term term, int mode, float thr, float &v, int *sg, int64_t *sc, WB &W, int g = 0,
+                              WalkCp *cp = nullptr) {
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-    int g = 0, buf = 0;
+    int buf = 0, ncp = 0;
     while (g <= gk) {
+        if (cp && ncp < kWalkCp) {  // uniform
+            if (tid == 0) {
+                cp->g[ncp] = g;
+                cp->v[ncp] = v;
+                cp->n = ncp + 1;
+            }
+            ++ncp;
+        }
         if ((mode != kWalkDrop && v == 0.0f) || (mode == kWalkDrop && !(v > 0.0f))) {  // no grid yet: one group
             const int64_t s = walk_group(v, term(gval[g]), g == gk ? ck : gcnt[g], mode, thr);
             if (s >= 0) {
@@ -547,10 +567,21 @@ __global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
     uint64_t keep = (uint64_t)P.n;  // the reference's candidate count (V)
     if (P.top_p < 1.0f) {          // :215-227
         float total = 0.0f;
-        walk_block(gval, gcnt, gpos, G - 1, gcnt[G - 1], eterm, kWalkSum, 0.0f, total, &sg, &sc, L.wb);
+        if (tid == 0) L.cp.n = 0;
+        __syncthreads();
+        walk_block(gval, gcnt, gpos, G - 1, gcnt[G - 1], eterm, kWalkSum, 0.0f, total, &sg, &sc, L.wb, 0, &L.cp);
+        __syncthreads();  // the checkpoints
         const float thr = P.top_p * total;
-        float acc = 0.0f;
-        const int64_t pos = walk_block(gval, gcnt, gpos, G - 1, gcnt[G - 1], eterm, kWalkReach, thr, acc, &sg, &sc, L.wb);
+        // The crossing adds the same terms in the same order as the total, and
+        // the running value never decreases: it lies past the last checkpoint
+        // still below thr, from which the walk resumes with that value.
+        int c = 0;
+        for (int j = 1; j < L.cp.n; ++j)
+            if (L.cp.v[j] < thr) c = j;
+        float acc = L.cp.n > 0 ? L.cp.v[c] : 0.0f;
+        const int gs = L.cp.n > 0 ? L.cp.g[c] : 0;
+        const int64_t pos =
+            walk_block(gval, gcnt, gpos, G - 1, gcnt[G - 1], eterm, kWalkReach, thr, acc, &sg, &sc, L.wb, gs);
         keep = pos >= 0 ? (uint64_t)pos + 1 : keep;
     }
     if (P.min_p > 0.0f) {  // :228-234: the first term below min_p within keep
