@@ -602,7 +602,20 @@ __global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
     const float inv_t = 1.0f / P.temp;
     auto wterm = [&](float x) { return zexpf_nb((x - mx) * inv_t); };
     float total = 0.0f;
-    walk_block(gval, gcnt, gpos, gk, ck, wterm, kWalkSum, 0.0f, total, &sg, &sc, L.wb);
+    int gs = 0;
+    if (inv_t == 1.0f && P.top_p < 1.0f) {
+        // (x - mx) * 1 is x - mx exactly: the weights are the top-p terms, and
+        // their total over keep continues the top-p total from its last
+        // checkpoint at or before the group holding entry keep - 1
+        int c = -1;
+        for (int j = 0; j < L.cp.n; ++j)
+            if (L.cp.g[j] <= gk) c = j;
+        if (c >= 0) {
+            total = L.cp.v[c];
+            gs = L.cp.g[c];
+        }
+    }
+    walk_block(gval, gcnt, gpos, gk, ck, wterm, kWalkSum, 0.0f, total, &sg, &sc, L.wb, gs);
     const float u0 = P.uniforms[2 * row];
     float r = u0 * total;
     if (walk_block(gval, gcnt, gpos, gk, ck, wterm, kWalkDrop, 0.0f, r, &sg, &sc, L.wb) < 0) {
