@@ -113,6 +113,26 @@ def test_softcap_late_select(ctx, oracle, kind, mask, cap, pen):
     assert not errs, "\n".join(errs[:20])
 
 
+@pytest.mark.parametrize("kind", ["normal", "huge"])
+@pytest.mark.parametrize("pen", [True, False])
+def test_softcap_late_select_bf16(ctx, oracle, kind, pen):
+    """The candidates-only softcap on bf16 rows (their own kernel instances)."""
+    rows, V = 16, 151936
+    rng = np.random.Generator(np.random.PCG64(3400 + (1 if kind == "huge" else 0) + (2 if pen else 0)))
+    x, hist, hl, m, ei, ed, ec = _inputs(rng, rows, V, "normal", pen, False, pen)
+    if kind == "huge":
+        x = (x * 100 + 500).astype(np.float32)
+    x = _bf16_round(x)
+    pk = dict(temp=0.8, top_k=40, top_p=0.95, min_p=0.05, final_logit_softcap=30.0)
+    if pen:
+        pk.update(repeat_penalty=1.1, freq_penalty=0.1, presence_penalty=0.2, penalty_last_n=128)
+    u = rng.random((rows, 2), dtype=np.float32)
+    g = gpu_sample(ctx, pk, x, u, hist, hl, m, ei, ed, ec, bf16=True)
+    o = oracle_sample(oracle, pk, x, u, hist, hl, m, ei, ed, ec)
+    errs = compare_sample(g, o, pk, V, f"softcap late bf16 {kind}")
+    assert not errs, "\n".join(errs[:20])
+
+
 @pytest.mark.parametrize("V", [32, 4096, 151936])
 def test_softcap_greedy_matches_oracle(ctx, oracle, V):
     """temp = 0 takes the argmax pass; capped ties (saturated logits) go to the
