@@ -44,6 +44,8 @@ def parse():
     ap.add_argument("--min-p", type=float, default=None,
                     help="override the config's min_p (config 5 with 0 is the whole-order nucleus case)")
     ap.add_argument("--top-k", type=int, default=None, help="override the config's top_k")
+    ap.add_argument("--spike", type=float, default=0.0,
+                    help="add this to one seeded entry per row (a dominant token: peaked rows)")
     ap.add_argument("--pruned", type=int, default=0,
                     help="pruned rows (sample path): 64 fixed + this many random groups of 8 ids per row are the "
                          "only logits (zi_sample_rows_pruned; the reference keeps 512); 0 = dense rows")
@@ -607,6 +609,15 @@ def main():
     if args.top_k is not None:
         w.params = dict(w.params, top_k=args.top_k)
         w.name += f"_k{args.top_k}"
+    if args.spike:
+        srng = np.random.Generator(np.random.PCG64(77))
+        cols = srng.integers(0, V, size=rows)
+        w.logits = w.logits.copy()
+        w.logits[np.arange(rows), cols] += np.float32(args.spike)
+        if w.bf16:
+            from zinfer_amd.workloads import _bf16_round
+            w.logits = _bf16_round(w.logits)
+        w.name += f"_spike{args.spike:g}"
     if args.config == 4:
         bench_entropy(args, w)
         return
