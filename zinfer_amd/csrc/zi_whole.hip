@@ -12,15 +12,16 @@
 // entries of its value, ascending id (the stable sort's tie rule).
 //
 // One 512-thread workgroup per flagged row:
-//  1. penalty bitset and hash in LDS; each penalized id's first inserter
-//     loads its logit (as in the prefix pass).
-//  2. read the row: the row max and second value, and a bitmap of the 16-bit
-//     order keys present among the unpenalized entries.
-//  3. the penalized values; the floor; ranks of the present keys at or above
-//     it (descending) from a suffix count over the bitmap words.
-//  4. read the row again: each entry's key rank gets a count.
-//  5. the group list: key groups and penalized entries (one group each)
-//     merged by value.
+//  1. penalty hash in LDS; each penalized id's first inserter loads its logit
+//     and keeps its count and delta.
+//  2-3. read the row: entries per 16-bit order key (two 16-bit counts per LDS
+//     word, 128 KB), penalized ids' raw entries then taken out; a count that
+//     overflowed (more than 65535 equal entries) shows as a short total.
+//  4. each thread takes its 128 keys' counts into registers: the row max and
+//     second value, the floor, the penalized entries above it.
+//  5. ranks of the present keys at or above the floor (descending, a suffix
+//     count over threads); the group list: key groups and penalized entries
+//     (one group each) merged by value.
 //  6. wave 0 walks the groups: the top-p total and crossing, min-p, the
 //     temperature total over keep, the draw.
 //  7. the drawn entry's id: the (j+1)-th entry, in id order, of its value.
@@ -46,29 +47,31 @@ struct WalkCp {
     int n;
 };
 
+constexpr int kKeyWords = 65536 / 2;  // 16-bit order keys, two 16-bit counts per word
+
 struct WholeLds {
-    uint32_t pbits[kMaxVocab / 32];  // penalized ids
     union {
-        struct {  // steps 1-3
+        struct {  // step 1: the penalty hash
             uint32_t key[kHashMax];
             uint32_t cnt[kHashMax];
             float delta[kHashMax];
+            uint32_t own[kHashMax];  // claimed by the id's first inserter
         } h;
-        struct {  // steps 5-7
+        uint32_t kc[kKeyWords];  // steps 2-4: entries per key, two 16-bit counts per word
+        struct {                 // steps 5-7, once every count is in registers
             float gval[kWholeGroups];
             uint32_t gcnt[kWholeGroups];
+            union {
+                struct {
+                    uint32_t bcnt[kWholeKeys];   // entries per key rank
+                    uint16_t bkey[kWholeKeys];   // key of each rank
+                } k;                             // step 5
+                uint32_t gpos[kWholeGroups];     // step 6: entries before each group
+                uint32_t vbits[kMaxVocab / 32];  // step 7: penalized ids whose value is the drawn one
+            } w;
+            uint32_t pbits[kMaxVocab / 32];  // step 7: penalized ids
         } g;
     } u;
-    union {
-        struct {                         // steps 2-5
-            uint32_t kbits[65536 / 32];  // present keys
-            uint2 kw[65536 / 32];        // per word: its present keys at or above the floor, and how many are in words above
-            uint32_t bcnt[kWholeKeys];   // entries per key rank
-            uint16_t bkey[kWholeKeys];   // key of each rank
-        } k;
-        uint32_t vbits[kMaxVocab / 32];  // step 7: penalized ids whose value is the drawn one
-        uint32_t gpos[kWholeGroups];     // step 6: entries before each group
-    } w;
     struct {  // block walks: the waves' total maps and first events, by chunk parity
         uint64_t inc0[2][kWaves], inc1[2][kWaves];
         uint32_t par[2][kWaves];
@@ -88,6 +91,8 @@ struct WholeLds {
     uint32_t tcnt[kMaxVocab / (8 * kThreads)];  // entries of the drawn value per 4096-id tile
     int npen, nsel;
     int found;
+    int k1, k2, c1;     // the highest present key, its count, the next present key
+    uint32_t ncnt, nsum;  // entries counted, and the sum of the key counts (a 16-bit count overflowed if they differ)
     uint32_t tok;
     float f[4];
     int64_t i64[4];
@@ -263,40 +268,43 @@ __global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
     const uint16_t *lrow = reinterpret_cast<const uint16_t *>(a.logits) + (int64_t)row * a.ld;
     const uint32_t *mrow = HAS_MASK ? a.mask + (int64_t)row * a.mask_ld : nullptr;
 
-    // 1. penalties: bitset, hash, owners
+    // 1. penalties: the window ids (counts) and the edits (deltas) in a hash;
+    //    the first inserter of each id owns it, loads its logit and keeps its
+    //    count and delta in registers (the hash's memory then holds the key
+    //    counts)
     uint32_t oid[kOwnSlots];
-    int oslot[kOwnSlots];
     uint32_t oraw[kOwnSlots];
+    uint32_t ocnt[kOwnSlots];
+    float odel[kOwnSlots];
 #pragma unroll
     for (int s = 0; s < kOwnSlots; ++s) {
         oid[s] = 0xFFFFFFFFu;
-        oslot[s] = 0;
         oraw[s] = 0u;
+        ocnt[s] = 0u;
+        odel[s] = 0.0f;
     }
-    RowPen rp;
-    rp.hs_log2 = 6;
     if constexpr (HAS_PEN) {
         PenRegs pr;
         pen_prefetch(a, row, pr);
-        rp = row_pen(a, row);
+        const RowPen rp = row_pen(a, row);
         pen_window(rp, pr);
-        for (int i = tid; i < (V + 31) / 32; i += kThreads) L.pbits[i] = 0u;
         for (int i = tid; i < kHashMax; i += kThreads) {
             L.u.h.key[i] = 0u;
             L.u.h.cnt[i] = 0u;
             L.u.h.delta[i] = 0.0f;
+            L.u.h.own[i] = 0u;
         }
         __syncthreads();
+        int oslot[kOwnSlots];
 #pragma unroll
         for (int s = 0; s < kOwnSlots; ++s) {
+            oslot[s] = -1;
             const uint32_t id = s < kWinPerThread ? pr.w[s] : pr.e;
             if (id < (uint32_t)V) {
-                const uint32_t bit = 1u << (id & 31);
-                const bool first = !(atomicOr(&L.pbits[id >> 5], bit) & bit);
                 const int h = pen_insert(L.u.h, id, rp.hs_log2);
                 if (s < kWinPerThread) atomicAdd(&L.u.h.cnt[h], 1u);
                 else L.u.h.delta[h] = pr.d;
-                if (first) {
+                if (atomicOr(&L.u.h.own[h], 1u) == 0u) {
                     oid[s] = id;
                     oslot[s] = h;
                 }
@@ -305,17 +313,34 @@ __global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
 #pragma unroll
         for (int s = 0; s < kOwnSlots; ++s)
             if (oid[s] != 0xFFFFFFFFu) oraw[s] = (uint32_t)lrow[oid[s]];
+        __syncthreads();  // counts and deltas complete
+#pragma unroll
+        for (int s = 0; s < kOwnSlots; ++s) {
+            if (oslot[s] >= 0) {
+                ocnt[s] = L.u.h.cnt[oslot[s]];
+                odel[s] = L.u.h.delta[oslot[s]];
+            }
+        }
+        __syncthreads();  // every read of the hash is done
     }
-    for (int i = tid; i < 65536 / 32; i += kThreads) L.w.k.kbits[i] = 0u;
+
+    // 2. the key counts, cleared
+    for (int i = tid; i < kKeyWords; i += kThreads) L.u.kc[i] = 0u;
     if (tid == 0) {
         L.npen = 0;
         L.nsel = 0;
         L.found = 0;
+        L.k1 = -1;
+        L.k2 = -1;
+        L.c1 = 0;
+        L.ncnt = 0u;
+        L.nsum = 0u;
     }
     __syncthreads();
 
-    // 2. row max / second (unpenalized entries), present keys
-    float t1 = -INFINITY, t2 = -INFINITY;
+    // 3. read the row: entries per 16-bit order key, every non-NaN entry
+    //    (penalized ones too: their raw entries leave the counts below)
+    uint32_t ncount = 0;
     for (int q0 = tid; q0 < nvec; q0 += kThreads * kWholeBatch) {
         uint4 rawb[kWholeBatch];
         uint32_t mwb[kWholeBatch];
@@ -332,26 +357,24 @@ __global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
 #pragma unroll
         for (int j = 0; j < kWholeBatch; ++j) {
             const int q = q0 + j * kThreads;
-            if (q >= nvec) break;
+            if (q >= nvec) continue;  // (not break: the loop stays unrolled, rawb in registers)
             float v[VEC];
             unpack<uint16_t>(rawb[j], v);
             const int id0 = q * VEC;
             const uint32_t mb = HAS_MASK ? mwb[j] >> (id0 & 31) : 0xFFu;
-            const uint32_t pb = HAS_PEN ? (L.pbits[id0 >> 5] >> (id0 & 31)) : 0u;
 #pragma unroll
             for (int e = 0; e < VEC; ++e) {
-                if (id0 + e >= V || ((pb >> e) & 1u)) continue;
+                if (id0 + e >= V) continue;
                 float x = v[e];
                 if (HAS_MASK && !((mb >> e) & 1u)) x = -INFINITY;
                 if (x != x) continue;  // NaN: no place in the order (outside the reference's contract)
-                top2_merge(t1, t2, x);
                 const uint32_t k = key16(x);
-                const uint32_t bit = 1u << (k & 31);
-                atomicOr(&L.w.k.kbits[k >> 5], bit);  // no return: nothing waits on it
+                atomicAdd(&L.u.kc[k >> 1], (k & 1u) ? 0x10000u : 1u);  // no return: nothing waits on it
+                ++ncount;
             }
         }
     }
-    // 3. penalized values
+    // the penalized entries: their raw entries out, their penalized values kept
     float pvs[kOwnSlots];
 #pragma unroll
     for (int s = 0; s < kOwnSlots; ++s) {
@@ -359,28 +382,83 @@ __global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
         if (HAS_PEN && oid[s] != 0xFFFFFFFFu) {
             float x = __uint_as_float(oraw[s] << 16);
             if (HAS_MASK && !((mrow[oid[s] >> 5] >> (oid[s] & 31)) & 1u)) x = -INFINITY;
-            x = pen_apply(x, L.u.h.cnt[oslot[s]], L.u.h.delta[oslot[s]], a);
-            pvs[s] = x;
-            if (x == x) top2_merge(t1, t2, x);
+            if (x == x) {
+                const uint32_t k = key16(x);
+                atomicSub(&L.u.kc[k >> 1], (k & 1u) ? 0x10000u : 1u);
+                --ncount;
+            }
+            pvs[s] = pen_apply(x, ocnt[s], odel[s], a);
         }
     }
+    __syncthreads();  // counts final
+
+    // 4. the counts into registers: this thread's 128 keys [128 tid, 128 tid
+    //    + 128), slot q = key - 128 tid, with its two highest present slots
+    constexpr int kKeyPer = 65536 / kThreads;  // 128
+    uint32_t cw[kKeyPer / 2];
+    uint32_t nsum = 0;
+    int st1 = -1, st2 = -1;  // slots (constants; the keys are formed after the loop)
+    uint32_t ct1 = 0;
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const float o1 = __shfl_xor(t1, o), o2 = __shfl_xor(t2, o);
-        t2 = fmaxf(fmaxf(t2, o2), fminf(t1, o1));
-        t1 = fmaxf(t1, o1);
+    for (int q4 = 0; q4 < kKeyPer / 8; ++q4) {
+        const uint4 t = reinterpret_cast<const uint4 *>(L.u.kc + tid * (kKeyPer / 2))[q4];
+        cw[4 * q4] = t.x;
+        cw[4 * q4 + 1] = t.y;
+        cw[4 * q4 + 2] = t.z;
+        cw[4 * q4 + 3] = t.w;
     }
-    if (lane == 0) {
-        L.wt1[wid] = t1;
-        L.wt2[wid] = t2;
-    }
-    __syncthreads();  // maxima; every read of the hash is done
-    float mx = L.wt1[0], second = L.wt2[0];
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) {
-        const float o1 = L.wt1[w], o2 = L.wt2[w];
-        second = fmaxf(fmaxf(second, o2), fminf(mx, o1));
-        mx = fmaxf(mx, o1);
+    for (int q = 0; q < kKeyPer; ++q) {  // keys ascend with q
+        const uint32_t c = (q & 1) ? (cw[q >> 1] >> 16) : (cw[q >> 1] & 0xFFFFu);
+        nsum += c;
+        if (c) {
+            st2 = st1;
+            st1 = q;
+            ct1 = c;
+        }
+    }
+    const int kt1 = st1 < 0 ? -1 : kKeyPer * tid + st1, kt2 = st2 < 0 ? -1 : kKeyPer * tid + st2;
+    // the packed words stay the only copy (the halves are extracted again
+    // where used, not kept apart across the phases)
+#pragma unroll
+    for (int j = 0; j < kKeyPer / 2; ++j) asm volatile("" : "+v"(cw[j]));
+    atomicAdd(&L.ncnt, ncount);
+    atomicAdd(&L.nsum, nsum);
+    atomicMax(&L.k1, kt1);
+    __syncthreads();
+    const int K1 = L.k1;
+    if (K1 >= 0 && kt1 == K1) L.c1 = (int)ct1;  // one thread holds each key
+    atomicMax(&L.k2, kt1 == K1 ? kt2 : kt1);
+    __syncthreads();  // every count is in registers; the memory is free
+    if (L.ncnt != L.nsum) return;  // a 16-bit count overflowed: the sorting pass (uniform)
+    float mx = -INFINITY, second = -INFINITY;  // the unpenalized entries' top two
+    if (K1 >= 0) {
+        mx = key16_value((uint32_t)K1);
+        if (L.c1 >= 2) second = mx;
+        else if (L.k2 >= 0) second = key16_value((uint32_t)L.k2);
+    }
+    {  // and the penalized values
+        float t1 = -INFINITY, t2 = -INFINITY;
+#pragma unroll
+        for (int s = 0; s < kOwnSlots; ++s)
+            if (pvs[s] == pvs[s]) top2_merge(t1, t2, pvs[s]);
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const float o1 = __shfl_xor(t1, o), o2 = __shfl_xor(t2, o);
+            t2 = fmaxf(fmaxf(t2, o2), fminf(t1, o1));
+            t1 = fmaxf(t1, o1);
+        }
+        if (lane == 0) {
+            L.wt1[wid] = t1;
+            L.wt2[wid] = t2;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const float o1 = L.wt1[w], o2 = L.wt2[w];
+            second = fmaxf(fmaxf(second, o2), fminf(mx, o1));
+            mx = fmaxf(mx, o1);
+        }
     }
     if (!__builtin_isfinite(mx)) return;  // the sorting pass handles it (uniform)
     // the floor: entries below it cannot reach keep nor change a sum
@@ -397,19 +475,18 @@ __global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
             L.pid[i] = oid[s];
         }
     }
-    // key ranks: present keys >= kmin, descending; each thread sums 4 words
-    uint32_t wc[4], mine = 0;
+    // 5. the present keys at or above the floor, ranked in descending order
+    //    (and the penalized ids' bitset, for step 7)
+    if (HAS_PEN)
+        for (int i = tid; i < (V + 31) / 32; i += kThreads) L.u.g.pbits[i] = 0u;
+    uint32_t mine = 0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t w = (uint32_t)(4 * tid + j);
-        uint32_t bits = L.w.k.kbits[w];
-        if (w * 32 + 31 < kmin) bits = 0u;
-        else if (w * 32 < kmin) bits &= ~0u << (kmin - w * 32);
-        L.w.k.kbits[w] = bits;
-        wc[j] = (uint32_t)__popc(bits);
-        mine += wc[j];
+    for (int q = 0; q < kKeyPer; ++q) {
+        const uint32_t c = (q & 1) ? (cw[q >> 1] >> 16) : (cw[q >> 1] & 0xFFFFu);
+        mine += (c && (uint32_t)(kKeyPer * tid + q) >= kmin) ? 1u : 0u;
     }
-    // suffix over threads (descending keys: higher threads first)
+#pragma unroll
+    for (int j = 0; j < kKeyPer / 2; ++j) asm volatile("" : "+v"(cw[j]));
     uint32_t incl = mine;  // inclusive over higher-or-equal lanes within the wave
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
@@ -417,87 +494,47 @@ __global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
         if (lane + o < 64) incl += y;
     }
     if (lane == 0) L.wsum[wid] = incl;
-    __syncthreads();
-    uint32_t above = incl - mine;  // in higher lanes of this wave
+    __syncthreads();  // wave sums; pbits cleared; penalized entries collected
+#pragma unroll
+    for (int s = 0; s < kOwnSlots; ++s)
+        if (HAS_PEN && oid[s] != 0xFFFFFFFFu) atomicOr(&L.u.g.pbits[oid[s] >> 5], 1u << (oid[s] & 31));
+    uint32_t rk = incl - mine;  // present keys in higher lanes of this wave, then in higher waves
 #pragma unroll
     for (int w = 0; w < kWaves; ++w)
-        if (w > wid) above += L.wsum[w];
+        if (w > wid) rk += L.wsum[w];
     uint32_t D = 0;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) D += L.wsum[w];
-    const int npen = L.npen;
     if (D > (uint32_t)kWholeKeys) return;  // too many distinct values: the sorting pass (uniform)
 #pragma unroll
-    for (int j = 3; j >= 0; --j) {  // words in descending order within this thread
-        const uint32_t w = (uint32_t)(4 * tid + j);
-        uint32_t bits = L.w.k.kbits[w];
-        L.w.k.kw[w] = make_uint2(bits, above);
-        uint32_t r = above;
-        while (bits) {  // highest key first
-            const int b = 31 - __clz(bits);
-            L.w.k.bkey[r] = (uint16_t)(w * 32 + (uint32_t)b);
-            L.w.k.bcnt[r] = 0u;
-            ++r;
-            bits &= ~(1u << b);
-        }
-        above += wc[j];
-    }
-    __syncthreads();
-
-    // 4. counts per key rank
-    for (int q0 = tid; q0 < nvec; q0 += kThreads * kWholeBatch) {
-        uint4 rawb[kWholeBatch];
-        uint32_t mwb[kWholeBatch];
-#pragma unroll
-        for (int j = 0; j < kWholeBatch; ++j) {  // every load first
-            const int q = q0 + j * kThreads;
-            rawb[j] = make_uint4(0u, 0u, 0u, 0u);
-            mwb[j] = 0u;
-            if (q < nvec) {
-                rawb[j] = *reinterpret_cast<const uint4 *>(lrow + q * VEC);
-                if (HAS_MASK) mwb[j] = mrow[(q * VEC) >> 5];
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < kWholeBatch; ++j) {
-            const int q = q0 + j * kThreads;
-            if (q >= nvec) break;
-            float v[VEC];
-            unpack<uint16_t>(rawb[j], v);
-            const int id0 = q * VEC;
-            const uint32_t mb = HAS_MASK ? mwb[j] >> (id0 & 31) : 0xFFu;
-            const uint32_t pb = HAS_PEN ? (L.pbits[id0 >> 5] >> (id0 & 31)) : 0u;
-#pragma unroll
-            for (int e = 0; e < VEC; ++e) {
-                if (id0 + e >= V || ((pb >> e) & 1u)) continue;
-                float x = v[e];
-                if (HAS_MASK && !((mb >> e) & 1u)) x = -INFINITY;
-                if (x != x) continue;
-                const uint32_t k = key16(x);
-                if (k < kmin) continue;
-                const uint2 kw = L.w.k.kw[k >> 5];  // one read: the word's keys and the count above it
-                atomicAdd(&L.w.k.bcnt[kw.y + (uint32_t)__popc(kw.x >> (k & 31) >> 1)], 1u);
-            }
+    for (int q = kKeyPer - 1; q >= 0; --q) {  // this thread's keys, highest first
+        const uint32_t c = (q & 1) ? (cw[q >> 1] >> 16) : (cw[q >> 1] & 0xFFFFu);
+        const uint32_t k = (uint32_t)(kKeyPer * tid + q);
+        if (c && k >= kmin) {
+            L.u.g.w.k.bkey[rk] = (uint16_t)k;
+            L.u.g.w.k.bcnt[rk] = c;
+            ++rk;
         }
     }
+    const int npen = L.npen;
     // penalized entries ranked by (value desc, id asc)
     for (int i = tid; i < npen; i += kThreads) {
         const float vi = L.pval[i];
         const uint32_t ii = L.pid[i];
-        int r = 0;
+        int rr = 0;
         for (int j = 0; j < npen; ++j) {
             const float vj = L.pval[j];
-            r += (vj > vi || (vj == vi && L.pid[j] < ii)) ? 1 : 0;
+            rr += (vj > vi || (vj == vi && L.pid[j] < ii)) ? 1 : 0;
         }
-        L.sval[r] = vi;
-        L.sid[r] = ii;
+        L.sval[rr] = vi;
+        L.sid[rr] = ii;
     }
-    __syncthreads();
+    __syncthreads();  // key ranks and penalized order complete
 
-    // 5. the group list, key groups and penalized entries merged by value
-    //    (a key group before the penalized entries of its value)
+    // the group list: key groups and penalized entries merged by value (a key
+    // group before the penalized entries of its value)
     for (int r = tid; r < (int)D; r += kThreads) {
-        const float vr = key16_value(L.w.k.bkey[r]);
+        const float vr = key16_value(L.u.g.w.k.bkey[r]);
         int lo = 0, hi = npen;  // penalized entries with value > vr
         while (lo < hi) {
             const int mid = (lo + hi) >> 1;
@@ -505,14 +542,14 @@ __global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
             else hi = mid;
         }
         L.u.g.gval[r + lo] = vr;
-        L.u.g.gcnt[r + lo] = L.w.k.bcnt[r];
+        L.u.g.gcnt[r + lo] = L.u.g.w.k.bcnt[r];
     }
     for (int p = tid; p < npen; p += kThreads) {
         const float vp = L.sval[p];
         int lo = 0, hi = (int)D;  // key groups with value >= vp
         while (lo < hi) {
             const int mid = (lo + hi) >> 1;
-            if (key16_value(L.w.k.bkey[mid]) >= vp) lo = mid + 1;
+            if (key16_value(L.u.g.w.k.bkey[mid]) >= vp) lo = mid + 1;
             else hi = mid;
         }
         L.u.g.gval[p + lo] = vp;
@@ -541,14 +578,14 @@ __global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
         for (int w = 0; w < wid; ++w) run += L.wsum[w];
         for (int k = 0; k < kPer; ++k)
             if (g0 + k < G) {
-                L.w.gpos[g0 + k] = run;
+                L.u.g.w.gpos[g0 + k] = run;
                 run += L.u.g.gcnt[g0 + k];
             }
         __syncthreads();
     }
     const float *gval = L.u.g.gval;
     const uint32_t *gcnt = L.u.g.gcnt;
-    const uint32_t *gpos = L.w.gpos;
+    const uint32_t *gpos = L.u.g.w.gpos;
     const uint64_t in_list = (uint64_t)gpos[G - 1] + gcnt[G - 1];  // entries in the group list
     // the group holding entry e - 1 and how many of its entries come before e
     auto cut = [&](uint64_t e, int &gk, uint32_t &ck) {
@@ -638,7 +675,7 @@ __global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
         unpack<uint16_t>(raw, v);
         const int id0 = q * VEC;
         const uint32_t mb = HAS_MASK ? mword >> (id0 & 31) : 0xFFu;
-        const uint32_t pb = HAS_PEN ? (L.pbits[id0 >> 5] >> (id0 & 31)) : 0u;
+        const uint32_t pb = HAS_PEN ? (L.u.g.pbits[id0 >> 5] >> (id0 & 31)) : 0u;
         uint32_t hit = 0u;
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
@@ -647,15 +684,15 @@ __global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
             if (HAS_MASK && !((mb >> e) & 1u)) x = -INFINITY;
             if (!((pb >> e) & 1u) && x == vt) hit |= 1u << e;
         }
-        if (HAS_PEN) hit |= (L.w.vbits[id0 >> 5] >> (id0 & 31)) & 0xFFu;  // penalized ones of value vt
+        if (HAS_PEN) hit |= (L.u.g.w.vbits[id0 >> 5] >> (id0 & 31)) & 0xFFu;  // penalized ones of value vt
         return hit;
     };
     for (int i = tid; i < ntile; i += kThreads) L.tcnt[i] = 0u;
     if (HAS_PEN) {
-        for (int i = tid; i < (V + 31) / 32; i += kThreads) L.w.vbits[i] = 0u;
+        for (int i = tid; i < (V + 31) / 32; i += kThreads) L.u.g.w.vbits[i] = 0u;
         __syncthreads();
         for (int p = tid; p < npen; p += kThreads)
-            if (L.sval[p] == vt) atomicOr(&L.w.vbits[L.sid[p] >> 5], 1u << (L.sid[p] & 31));
+            if (L.sval[p] == vt) atomicOr(&L.u.g.w.vbits[L.sid[p] >> 5], 1u << (L.sid[p] & 31));
     }
     __syncthreads();
     for (int t0 = 0; t0 < ntile; t0 += kWholeBatch) {
