@@ -17,11 +17,11 @@
 //  2-3. read the row: entries per 16-bit order key (two 16-bit counts per LDS
 //     word, 128 KB), penalized ids' raw entries then taken out; a count that
 //     overflowed (more than 65535 equal entries) shows as a short total.
-//  4. each thread takes its 128 keys' counts into registers: the row max and
-//     second value, the floor, the penalized entries above it.
+//  4. each thread reads its 128 keys' counts: the row max and second value,
+//     the floor, the penalized entries above it.
 //  5. ranks of the present keys at or above the floor (descending, a suffix
-//     count over threads); the group list: key groups and penalized entries
-//     (one group each) merged by value.
+//     count over threads, into arrays beside the counts); the group list: key
+//     groups and penalized entries (one group each) merged by value.
 //  6. wave 0 walks the groups: the top-p total and crossing, min-p, the
 //     temperature total over keep, the draw.
 //  7. the drawn entry's id: the (j+1)-th entry, in id order, of its value.
@@ -35,7 +35,7 @@
 namespace zi {
 
 constexpr int kWholeKeys = 4096;                   // distinct bf16 values above the floor
-constexpr int kWholePen = kOwnSlots * kThreads;    // penalized entries (window + edits), one per owner slot
+constexpr int kWholePen = kMaxWin + kMaxEdits;      // penalized entries (distinct window and edit ids)
 constexpr int kWholeGroups = kWholeKeys + kWholePen;
 constexpr int kWholeBatch = 16;  // row vectors in flight per thread
 
@@ -57,21 +57,19 @@ struct WholeLds {
             float delta[kHashMax];
             uint32_t own[kHashMax];  // claimed by the id's first inserter
         } h;
-        uint32_t kc[kKeyWords];  // steps 2-4: entries per key, two 16-bit counts per word
-        struct {                 // steps 5-7, once every count is in registers
+        uint32_t kc[kKeyWords];  // steps 2-5: entries per key, two 16-bit counts per word
+        struct {                 // steps 5-6
             float gval[kWholeGroups];
             uint32_t gcnt[kWholeGroups];
             union {
-                struct {
-                    uint32_t bcnt[kWholeKeys];   // entries per key rank
-                    uint16_t bkey[kWholeKeys];   // key of each rank
-                } k;                             // step 5
                 uint32_t gpos[kWholeGroups];     // step 6: entries before each group
                 uint32_t vbits[kMaxVocab / 32];  // step 7: penalized ids whose value is the drawn one
             } w;
-            uint32_t pbits[kMaxVocab / 32];  // step 7: penalized ids
         } g;
+        uint32_t pbits[kMaxVocab / 32];  // step 7: penalized ids (over the group list, no longer read)
     } u;
+    uint16_t bkey[kWholeKeys];  // step 5: key of each rank
+    uint16_t bcnt[kWholeKeys];  // entries per key rank (at most 65535: step 4 checks)
     struct {  // block walks: the waves' total maps and first events, by chunk parity
         uint64_t inc0[2][kWaves], inc1[2][kWaves];
         uint32_t par[2][kWaves];
@@ -82,10 +80,8 @@ struct WholeLds {
         int first;
     } wb;
     WalkCp cp;                   // the top-p total's checkpoints
-    float pval[kWholePen];       // penalized entries: value, id (then sorted by value desc, id asc)
+    float pval[kWholePen];       // penalized entries: value, id (sorted in place by value desc, id asc)
     uint32_t pid[kWholePen];
-    float sval[kWholePen];
-    uint32_t sid[kWholePen];
     float wt1[kWaves], wt2[kWaves];
     uint32_t wsum[kWaves];
     uint32_t tcnt[kMaxVocab / (8 * kThreads)];  // entries of the drawn value per 4096-id tile
@@ -392,36 +388,32 @@ __global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
     }
     __syncthreads();  // counts final
 
-    // 4. the counts into registers: this thread's 128 keys [128 tid, 128 tid
-    //    + 128), slot q = key - 128 tid, with its two highest present slots
+    // 4. this thread's 128 keys [128 tid, 128 tid + 128) (slot q = key - 128
+    //    tid): the two highest present, and the sum of the counts
     constexpr int kKeyPer = 65536 / kThreads;  // 128
-    uint32_t cw[kKeyPer / 2];
+    const uint4 *kc4 = reinterpret_cast<const uint4 *>(L.u.kc + tid * (kKeyPer / 2));
+    auto count_at = [](const uint4 &t, int q) -> uint32_t {  // slot q of a 16-byte group of 8 slots
+        const uint32_t w = (q >> 1) == 0 ? t.x : (q >> 1) == 1 ? t.y : (q >> 1) == 2 ? t.z : t.w;
+        return (q & 1) ? (w >> 16) : (w & 0xFFFFu);
+    };
     uint32_t nsum = 0;
-    int st1 = -1, st2 = -1;  // slots (constants; the keys are formed after the loop)
+    int st1 = -1, st2 = -1;
     uint32_t ct1 = 0;
 #pragma unroll
-    for (int q4 = 0; q4 < kKeyPer / 8; ++q4) {
-        const uint4 t = reinterpret_cast<const uint4 *>(L.u.kc + tid * (kKeyPer / 2))[q4];
-        cw[4 * q4] = t.x;
-        cw[4 * q4 + 1] = t.y;
-        cw[4 * q4 + 2] = t.z;
-        cw[4 * q4 + 3] = t.w;
-    }
+    for (int q8 = 0; q8 < kKeyPer / 8; ++q8) {  // keys ascend with the slot
+        const uint4 t = kc4[q8];
 #pragma unroll
-    for (int q = 0; q < kKeyPer; ++q) {  // keys ascend with q
-        const uint32_t c = (q & 1) ? (cw[q >> 1] >> 16) : (cw[q >> 1] & 0xFFFFu);
-        nsum += c;
-        if (c) {
-            st2 = st1;
-            st1 = q;
-            ct1 = c;
+        for (int q = 0; q < 8; ++q) {
+            const uint32_t c = count_at(t, q);
+            nsum += c;
+            if (c) {
+                st2 = st1;
+                st1 = 8 * q8 + q;
+                ct1 = c;
+            }
         }
     }
     const int kt1 = st1 < 0 ? -1 : kKeyPer * tid + st1, kt2 = st2 < 0 ? -1 : kKeyPer * tid + st2;
-    // the packed words stay the only copy (the halves are extracted again
-    // where used, not kept apart across the phases)
-#pragma unroll
-    for (int j = 0; j < kKeyPer / 2; ++j) asm volatile("" : "+v"(cw[j]));
     atomicAdd(&L.ncnt, ncount);
     atomicAdd(&L.nsum, nsum);
     atomicMax(&L.k1, kt1);
@@ -429,7 +421,7 @@ __global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
     const int K1 = L.k1;
     if (K1 >= 0 && kt1 == K1) L.c1 = (int)ct1;  // one thread holds each key
     atomicMax(&L.k2, kt1 == K1 ? kt2 : kt1);
-    __syncthreads();  // every count is in registers; the memory is free
+    __syncthreads();
     if (L.ncnt != L.nsum) return;  // a 16-bit count overflowed: the sorting pass (uniform)
     float mx = -INFINITY, second = -INFINITY;  // the unpenalized entries' top two
     if (K1 >= 0) {
@@ -476,17 +468,14 @@ __global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
         }
     }
     // 5. the present keys at or above the floor, ranked in descending order
-    //    (and the penalized ids' bitset, for step 7)
-    if (HAS_PEN)
-        for (int i = tid; i < (V + 31) / 32; i += kThreads) L.u.g.pbits[i] = 0u;
     uint32_t mine = 0;
 #pragma unroll
-    for (int q = 0; q < kKeyPer; ++q) {
-        const uint32_t c = (q & 1) ? (cw[q >> 1] >> 16) : (cw[q >> 1] & 0xFFFFu);
-        mine += (c && (uint32_t)(kKeyPer * tid + q) >= kmin) ? 1u : 0u;
-    }
+    for (int q8 = 0; q8 < kKeyPer / 8; ++q8) {
+        const uint4 t = kc4[q8];
 #pragma unroll
-    for (int j = 0; j < kKeyPer / 2; ++j) asm volatile("" : "+v"(cw[j]));
+        for (int q = 0; q < 8; ++q)
+            mine += (count_at(t, q) && (uint32_t)(kKeyPer * tid + 8 * q8 + q) >= kmin) ? 1u : 0u;
+    }
     uint32_t incl = mine;  // inclusive over higher-or-equal lanes within the wave
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
@@ -494,10 +483,7 @@ __global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
         if (lane + o < 64) incl += y;
     }
     if (lane == 0) L.wsum[wid] = incl;
-    __syncthreads();  // wave sums; pbits cleared; penalized entries collected
-#pragma unroll
-    for (int s = 0; s < kOwnSlots; ++s)
-        if (HAS_PEN && oid[s] != 0xFFFFFFFFu) atomicOr(&L.u.g.pbits[oid[s] >> 5], 1u << (oid[s] & 31));
+    __syncthreads();  // wave sums; penalized entries collected
     uint32_t rk = incl - mine;  // present keys in higher lanes of this wave, then in higher waves
 #pragma unroll
     for (int w = 0; w < kWaves; ++w)
@@ -507,49 +493,71 @@ __global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
     for (int w = 0; w < kWaves; ++w) D += L.wsum[w];
     if (D > (uint32_t)kWholeKeys) return;  // too many distinct values: the sorting pass (uniform)
 #pragma unroll
-    for (int q = kKeyPer - 1; q >= 0; --q) {  // this thread's keys, highest first
-        const uint32_t c = (q & 1) ? (cw[q >> 1] >> 16) : (cw[q >> 1] & 0xFFFFu);
-        const uint32_t k = (uint32_t)(kKeyPer * tid + q);
-        if (c && k >= kmin) {
-            L.u.g.w.k.bkey[rk] = (uint16_t)k;
-            L.u.g.w.k.bcnt[rk] = c;
-            ++rk;
+    for (int q8 = kKeyPer / 8 - 1; q8 >= 0; --q8) {  // this thread's keys, highest first
+        const uint4 t = kc4[q8];
+#pragma unroll
+        for (int q = 7; q >= 0; --q) {
+            const uint32_t c = count_at(t, q);
+            const uint32_t k = (uint32_t)(kKeyPer * tid + 8 * q8 + q);
+            if (c && k >= kmin) {
+                L.bkey[rk] = (uint16_t)k;
+                L.bcnt[rk] = (uint16_t)c;
+                ++rk;
+            }
         }
     }
     const int npen = L.npen;
-    // penalized entries ranked by (value desc, id asc)
-    for (int i = tid; i < npen; i += kThreads) {
-        const float vi = L.pval[i];
-        const uint32_t ii = L.pid[i];
-        int rr = 0;
-        for (int j = 0; j < npen; ++j) {
-            const float vj = L.pval[j];
-            rr += (vj > vi || (vj == vi && L.pid[j] < ii)) ? 1 : 0;
+    {  // penalized entries sorted in place by (value desc, id asc): ranks, then moves
+        float pv[kWholePen / kThreads + 1];
+        uint32_t pi[kWholePen / kThreads + 1];
+        int pr[kWholePen / kThreads + 1];
+#pragma unroll
+        for (int u = 0; u < kWholePen / kThreads + 1; ++u) {
+            const int i = tid + u * kThreads;
+            pr[u] = -1;
+            pv[u] = 0.0f;
+            pi[u] = 0u;
+            if (i < npen) {
+                pv[u] = L.pval[i];
+                pi[u] = L.pid[i];
+                int r = 0;
+                for (int j = 0; j < npen; ++j) {
+                    const float vj = L.pval[j];
+                    r += (vj > pv[u] || (vj == pv[u] && L.pid[j] < pi[u])) ? 1 : 0;
+                }
+                pr[u] = r;
+            }
         }
-        L.sval[rr] = vi;
-        L.sid[rr] = ii;
+        __syncthreads();  // every rank computed; key ranks stored; every count read
+#pragma unroll
+        for (int u = 0; u < kWholePen / kThreads + 1; ++u) {
+            if (pr[u] >= 0) {
+                L.pval[pr[u]] = pv[u];
+                L.pid[pr[u]] = pi[u];
+            }
+        }
     }
-    __syncthreads();  // key ranks and penalized order complete
+    __syncthreads();  // penalized order complete
 
     // the group list: key groups and penalized entries merged by value (a key
     // group before the penalized entries of its value)
     for (int r = tid; r < (int)D; r += kThreads) {
-        const float vr = key16_value(L.u.g.w.k.bkey[r]);
+        const float vr = key16_value(L.bkey[r]);
         int lo = 0, hi = npen;  // penalized entries with value > vr
         while (lo < hi) {
             const int mid = (lo + hi) >> 1;
-            if (L.sval[mid] > vr) lo = mid + 1;
+            if (L.pval[mid] > vr) lo = mid + 1;
             else hi = mid;
         }
         L.u.g.gval[r + lo] = vr;
-        L.u.g.gcnt[r + lo] = L.u.g.w.k.bcnt[r];
+        L.u.g.gcnt[r + lo] = L.bcnt[r];
     }
     for (int p = tid; p < npen; p += kThreads) {
-        const float vp = L.sval[p];
+        const float vp = L.pval[p];
         int lo = 0, hi = (int)D;  // key groups with value >= vp
         while (lo < hi) {
             const int mid = (lo + hi) >> 1;
-            if (key16_value(L.u.g.w.k.bkey[mid]) >= vp) lo = mid + 1;
+            if (key16_value(L.bkey[mid]) >= vp) lo = mid + 1;
             else hi = mid;
         }
         L.u.g.gval[p + lo] = vp;
@@ -663,7 +671,7 @@ __global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
     const float vt = gval[sg];
     int64_t idx = sc;
     for (int g = sg - 1; g >= 0 && gval[g] == vt; --g) idx += gcnt[g];
-    __syncthreads();  // every thread is done with gpos (its space becomes vbits)
+    __syncthreads();  // every thread is done with the group list and gpos (their space: pbits, vbits)
 
     // 7. the drawn entry's id: the (idx+1)-th entry of value vt in id order.
     //    One read of the row counts each 4096-id tile's entries of value vt
@@ -675,7 +683,7 @@ __global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
         unpack<uint16_t>(raw, v);
         const int id0 = q * VEC;
         const uint32_t mb = HAS_MASK ? mword >> (id0 & 31) : 0xFFu;
-        const uint32_t pb = HAS_PEN ? (L.u.g.pbits[id0 >> 5] >> (id0 & 31)) : 0u;
+        const uint32_t pb = HAS_PEN ? (L.u.pbits[id0 >> 5] >> (id0 & 31)) : 0u;
         uint32_t hit = 0u;
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
@@ -688,11 +696,17 @@ __global__ __launch_bounds__(kThreads) void whole_kernel(ExactParams P) {
         return hit;
     };
     for (int i = tid; i < ntile; i += kThreads) L.tcnt[i] = 0u;
-    if (HAS_PEN) {
-        for (int i = tid; i < (V + 31) / 32; i += kThreads) L.u.g.w.vbits[i] = 0u;
+    if (HAS_PEN) {  // penalized ids, and those whose penalized value is vt
+        for (int i = tid; i < (V + 31) / 32; i += kThreads) {
+            L.u.g.w.vbits[i] = 0u;
+            L.u.pbits[i] = 0u;
+        }
         __syncthreads();
         for (int p = tid; p < npen; p += kThreads)
-            if (L.sval[p] == vt) atomicOr(&L.u.g.w.vbits[L.sid[p] >> 5], 1u << (L.sid[p] & 31));
+            if (L.pval[p] == vt) atomicOr(&L.u.g.w.vbits[L.pid[p] >> 5], 1u << (L.pid[p] & 31));
+#pragma unroll
+        for (int s = 0; s < kOwnSlots; ++s)
+            if (oid[s] != 0xFFFFFFFFu) atomicOr(&L.u.pbits[oid[s] >> 5], 1u << (oid[s] & 31));
     }
     __syncthreads();
     for (int t0 = 0; t0 < ntile; t0 += kWholeBatch) {
