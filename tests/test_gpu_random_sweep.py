@@ -17,7 +17,7 @@ from zinfer_amd.workloads import _bf16_round, pack_mask
 
 pytestmark = pytest.mark.gpu
 
-N_CASES = 96
+N_CASES = 160
 
 
 def _draw(seed):
