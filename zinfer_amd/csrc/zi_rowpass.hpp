@@ -820,7 +820,7 @@ __device__ __forceinline__ void rank_count(const uint64_t *keys, const float *va
 #pragma unroll
             for (int q = 0; q < 8; ++q) c += (uint32_t)(keys[j + q] > mine);
         }
-        for (; j < n; ++j) c += (uint32_t)(keys[j] > mine);
+        for (; j < n && c < (uint32_t)k; ++j) c += (uint32_t)(keys[j] > mine);
         if (c < (uint32_t)k) {
             st_agent(&out.key[c], mine);
             st_agent(&out.val[c], vals[i]);
