@@ -367,9 +367,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
 #pragma unroll
             for (int e = 1; e < VEC; ++e) m = fmaxf(m, v[e]);
             lmax = fmaxf(lmax, m);
-            if (m > ref + kRefLag) {
-                S = S * __builtin_amdgcn_exp2f((ref - m) * kLog2e);
-                ref = m;
+            const bool up = m > ref + kRefLag;
+            if (ballot(up)) {  // a wave-uniform branch: taken about once per lane, so the rescale is not paid per vector
+                if (up) {
+                    S = S * __builtin_amdgcn_exp2f((ref - m) * kLog2e);
+                    ref = m;
+                }
+                asm volatile("" : "+v"(S), "+v"(ref));  // keeps the branch (not flattened into selects)
             }
 #pragma unroll
             for (int e = 0; e < VEC; ++e) S = S + __builtin_amdgcn_exp2f((v[e] - ref) * kLog2e);
