@@ -9,6 +9,8 @@ passes, the candidates-only softcap) in combinations the hand-written cases
 do not pin down one by one.  Bar: token ids, margins, uniforms consumed and
 keep bit-exact; with candidate outputs also the kept ids, values and
 probabilities, exactly as in the other parity files."""
+import os
+
 import numpy as np
 import pytest
 
@@ -17,7 +19,7 @@ from zinfer_amd.workloads import _bf16_round, pack_mask
 
 pytestmark = pytest.mark.gpu
 
-N_CASES = 160
+N_CASES = int(os.environ.get("ZI_SWEEP_CASES", "160"))  # seeds 0 .. N_CASES - 1
 
 
 def _draw(seed):
