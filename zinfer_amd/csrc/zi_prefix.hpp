@@ -170,7 +170,8 @@ __device__ __forceinline__ void prefix_prep(const RowSource &a, const PrefixLds 
         for (int e = 0; e < VEC; ++e) v[e] = ((mb >> e) & 1u) ? v[e] : -INFINITY;
     }
     const int lim = lim_id - id0;
-    if (HAS_PEN && lim > 0) {
+    // (a word passed in is in bounds for any id0; ids past lim_id go to -inf below either way)
+    if (HAS_PEN && (pword != nullptr || lim > 0)) {
         const uint32_t pb = ((pword ? *pword : L.bits[id0 >> 5]) >> (id0 & 31)) & ((1u << VEC) - 1u);
         if (pb) {
 #pragma unroll
